@@ -1,0 +1,232 @@
+"""Benchmark of the gfx950 GEMM hot path (one MI355X).
+
+Metric: TFLOPS and fraction of the dense MFMA peak for the
+4096x4096x8192 NT GEMM in fp16 (headline ``value``), bf8 and mxfp4.
+
+A "step" is one GEMM launch over one set of synthetic operands already
+resident in HBM.  The operands rotate over several sets (>= 512 MiB in total)
+so every launch starts with cold caches, as in the reference's protocol
+(kernels/gemm/intra_wave/a16w16/bench.py:190-241).  Timing: W untimed warm-up
+launches, then K launches bracketed by synchronize + HIP events on the launch
+stream; ms_per_step is the average launch time and TFLOPS = 2*M*N*K / t.
+
+The JSON line also carries the roofline of the dominant kernel (MFMA-bound:
+achieved TFLOP/s vs the published dense peak) with the HBM traffic per launch
+read from the committed rocprof counter summary when present, the other
+dtypes and the stream-K shapes, and a CPU baseline: the oracle's fp32 GEMM
+of the dequantized operands timed on this host on a bounded row sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+# Published dense MFMA peaks of one MI355X, TFLOP/s.
+PEAK = {"fp16": 2500.0, "bf16": 2500.0, "bf8": 5000.0, "mxfp4": 10100.0}
+# The reference's published MI355X numbers for the same shapes (4-wave,
+# kernels/gemm/intra_wave/a16w16/v9_beyond_hotloop/README.md:180,
+# kernels/gemm/inter_wave/a8w8/README.md:61, kernels/gemm/inter_wave/a4w4/v0_sliceMN/README.md:60).
+REFERENCE_TFLOPS = {"fp16": 1608.0, "bf8": 3215.0, "mxfp4": 4986.0}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--dtypes", default="fp16,bf8,mxfp4", help="comma list of fp16,bf16,bf8,mxfp4")
+    p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
+    p.add_argument("--cpu-baseline", type=int, default=1)
+    p.add_argument("--rotate-mb", type=int, default=512)
+    p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
+    return p.parse_args()
+
+
+def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
+    """Returns (launch(i) -> None, bytes per set)."""
+    import torch
+
+    from gfx950_gluon_tutorials_amd import quant
+    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a4w4 import matmul as m4
+    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a8w8 import matmul as m8
+    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as m16
+
+    gen = torch.Generator().manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        if dtype in ("fp16", "bf16"):
+            tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+            a = (torch.randn(M, K, generator=gen) * 0.1).to(tdt).to(dev)
+            b = (torch.randn(N, K, generator=gen) * 0.1).to(tdt).to(dev)
+            c = torch.empty(M, N, dtype=tdt, device=dev)
+            sets.append((a, b.T, c))
+        elif dtype == "bf8":
+            qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=gen).to(dev))
+            qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=gen).to(dev))
+            sets.append((qa, qb.T, sa, sb))
+        elif dtype == "mxfp4":
+            pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=gen).to(dev))
+            pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=gen).to(dev))
+            sets.append((pa, pb, sa, sb))
+        else:
+            raise ValueError(dtype)
+
+    def launch(i, schedule="dp"):
+        s = sets[i % len(sets)]
+        if dtype in ("fp16", "bf16"):
+            m16(s[0], s[1], s[2], schedule=schedule)
+        elif dtype == "bf8":
+            m8(s[0], s[1], a_scale=s[2], b_scale=s[3], out_dtype=torch.bfloat16, schedule=schedule)
+        else:
+            m4(s[0], s[1], s[2], s[3], schedule=schedule)
+
+    return launch
+
+
+def set_bytes(dtype, M, N, K):
+    if dtype in ("fp16", "bf16"):
+        return (M * K + N * K + M * N) * 2
+    if dtype == "bf8":
+        return M * K + N * K + 2 * M * N
+    return (M * K + N * K) // 2 + (M + N) * K // 32 + 2 * M * N
+
+
+def time_case(launch, steps, warmup, schedule="dp"):
+    import torch
+
+    for i in range(warmup):
+        launch(i, schedule)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        launch(i, schedule)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per launch
+
+
+def cpu_baseline(dtype: str, M: int, N: int, K: int, seed: int):
+    """The oracle's fp32 GEMM of the dequantized operands on this host, on a
+    row sample sized to a few seconds; TFLOPS scaled per FLOP."""
+    import numpy as np
+
+    from oracle import gemm_ref as R
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
+    except Exception:  # threadpoolctl missing: report the visible cores
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(seed)
+    rows = 512
+    a = rng.standard_normal((rows, K), dtype=np.float32) * 0.1
+    b = rng.standard_normal((N, K), dtype=np.float32) * 0.1
+    if dtype == "fp16":
+        a = a.astype(np.float16).astype(np.float32)
+        b = b.astype(np.float16).astype(np.float32)
+    R.gemm_f32(a[:64], b)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        R.gemm_f32(a, b)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    tflops = 2.0 * rows * N * K / t / 1e12
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"fp32 GEMM of dequantized operands, {rows}x{N}x{K} rows of the {M}x{N}x{K} workload, "
+                  f"median of 3 (oracle.gemm_ref.gemm_f32, numpy BLAS)",
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def load_traffic(key: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    import torch
+
+    dev = torch.device("cuda:0")
+    M = N = 4096
+    K = 8192
+    dtypes = [d for d in args.dtypes.split(",") if d]
+    if args.only:
+        dtypes = [args.only]
+    seeds = {"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3}
+    results = {}
+    for dt in dtypes:
+        nsets = max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, M, N, K)))
+        launch = make_case(dt, M, N, K, seeds[dt], dev, nsets)
+        ms = time_case(launch, args.steps, args.warmup)
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        results[dt] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
+                       "reference_tflops": REFERENCE_TFLOPS.get(dt), "rotating_sets": nsets}
+        print(f"# {dt}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak", flush=True)
+        del launch
+        torch.cuda.empty_cache()
+    sk = {}
+    if args.streamk and not args.only:
+        for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192)]:
+            launch = make_case("fp16", m, n, k, 4, dev, 2)
+            ms_dp = time_case(launch, max(10, args.steps // 4), 3, "dp")
+            ms_sk = time_case(launch, max(10, args.steps // 4), 3, "streamk")
+            flop = 2.0 * m * n * k
+            sk[f"{m}x{n}x{k}"] = {"dp_tflops": round(flop / ms_dp / 1e9, 2), "sk_tflops": round(flop / ms_sk / 1e9, 2),
+                                  "dp_ms": round(ms_dp, 5), "sk_ms": round(ms_sk, 5)}
+            print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f} TFLOPS", flush=True)
+            del launch
+            torch.cuda.empty_cache()
+    head = "fp16" if "fp16" in results else dtypes[0]
+    r = results[head]
+    line = {
+        "metric": "TFLOPS & % of MFMA peak, 4096x4096x8192 fp16/bf8/mxfp4, 1xMI355X",
+        "value": r["tflops"],
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(r["tflops"] / REFERENCE_TFLOPS[head], 4) if head in REFERENCE_TFLOPS else None,
+        "dtype": head,
+        "data": "synthetic",
+        "config": {"workload": f"{head} NT GEMM C=A.B^T, M=N=4096, K=8192, 256x256 tiles, data-parallel, 4-wave; "
+                               f"operands rotate over {r['rotating_sets']} resident sets",
+                   "M": M, "N": N, "K": K},
+        "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK[head], "unit": "TFLOP/s",
+                     "frac": r["frac_of_peak"], "traffic": load_traffic(f"{head}_{M}x{N}x{K}")},
+        "per_dtype": results,
+        "streamk": sk,
+    }
+    if args.cpu_baseline and not args.only:
+        line["cpu_baseline"] = cpu_baseline(head, M, N, K, seeds[head])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

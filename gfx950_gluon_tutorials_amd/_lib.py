@@ -1,0 +1,105 @@
+"""ctypes binding of the C ABI in ``include/gfx950_gemm.h``.
+
+The library is loaded from this package directory (built by ``build.py``).
+There is no fallback: if it is missing the import of a wrapper succeeds but
+the first call raises, so a GPU run can never silently fall back to torch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+LIB_PATH = _build.LIB_PATH
+
+# Status codes (gfx950_gemm.h).
+G9_OK = 0
+G9_ERR_SHAPE = 1
+G9_ERR_LAYOUT = 2
+G9_ERR_DTYPE = 3
+G9_ERR_SCHEDULE = 4
+G9_ERR_WORKSPACE = 5
+G9_ERR_HIP = 6
+
+# Element types.
+G9_F16 = 0
+G9_BF16 = 1
+G9_BF8 = 2
+G9_FP4 = 3
+
+# Schedules.
+G9_SCHED_DP = 0
+G9_SCHED_SK = 1
+
+SCHEDULES = {"dp": G9_SCHED_DP, "data_parallel": G9_SCHED_DP, "sk": G9_SCHED_SK, "streamk": G9_SCHED_SK}
+
+# Exported symbols and their signatures; the CPU test checks the library
+# exports exactly these.
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+SIGNATURES = {
+    "g9_gemm_a16w16": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                              _int, _int, _int, _vp, _sz, _vp]),
+    "g9_gemm_a8w8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _vp, _vp, _int, _int, _int, _vp, _sz, _vp]),
+    "g9_gemm_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]),
+    "g9_workspace_size": (_sz, [_int, _i64, _i64, _i64, _int, _int]),
+    "g9_workspace_init": (_int, [_vp, _sz, _vp]),
+    "g9_workspace_error": (_int, [_vp, _sz, _vp, ctypes.POINTER(_int)]),
+    "g9_kernel_name": (ctypes.c_char_p, [_int, _int, _int, _int]),
+    "g9_status_string": (ctypes.c_char_p, [_int]),
+    "g9_streamk_workgroups": (_int, []),
+    "g9_version": (_int, []),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load():
+    """Returns the loaded library, raising if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise LibraryMissing(
+                    f"{LIB_PATH} is not built; run `python -m gfx950_gluon_tutorials_amd.build`"
+                )
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def status_text(code: int) -> str:
+    return load().g9_status_string(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    """Maps a C status code to the Python exception a caller expects."""
+    if code == G9_OK:
+        return
+    msg = f"{what}: {status_text(code)} (status {code})"
+    if code in (G9_ERR_SHAPE, G9_ERR_LAYOUT, G9_ERR_DTYPE, G9_ERR_SCHEDULE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def kernel_name(dtype: int, out_dtype: int, schedule: int, waves: int) -> str | None:
+    name = load().g9_kernel_name(dtype, out_dtype, schedule, waves)
+    return name.decode() if name else None

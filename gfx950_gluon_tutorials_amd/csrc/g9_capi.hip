@@ -1,0 +1,309 @@
+// extern "C" entry points of the gfx950 GEMM library (declared in
+// include/gfx950_gemm.h).  Each validates shapes, strides and alignment,
+// fills a GemmParams and launches one named kernel on the caller's stream.
+#include <atomic>
+#include <mutex>
+
+#include "../../include/gfx950_gemm.h"
+#include "g9_gemm_4w.hpp"
+
+using namespace g9;
+
+// ---------------------------------------------------------------------------
+// Named kernels: one symbol per (operand type, output type, schedule, waves) so
+// profilers can filter on a stable substring.
+// ---------------------------------------------------------------------------
+#define G9_ATTRS __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+
+#define G9_DEFINE_4W(NAME, OP, OUT)                                                         \
+  extern "C" __global__ G9_ATTRS void NAME##_dp_4w(GemmParams p) { gemm_dp_4w<OP, OUT>(p); } \
+  extern "C" __global__ G9_ATTRS void NAME##_sk_4w(GemmParams p) { gemm_sk_4w<OP, OUT>(p); }
+
+G9_DEFINE_4W(g9_a16w16_f16, Op::F16, OUT_F16)
+G9_DEFINE_4W(g9_a16w16_bf16, Op::BF16, OUT_BF16)
+G9_DEFINE_4W(g9_a8w8_f16out, Op::BF8, OUT_F16)
+G9_DEFINE_4W(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
+G9_DEFINE_4W(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
+G9_DEFINE_4W(g9_a4w4_f16out, Op::FP4, OUT_F16)
+
+typedef void (*KernelFn)(GemmParams);
+
+namespace {
+
+struct KernelEntry {
+  int dtype, out, sched, waves;
+  KernelFn fn;
+  const char* name;
+};
+
+#define G9_ENTRY(DT, OUT, NAME)                                             \
+  {DT, OUT, G9_SCHED_DP, 4, NAME##_dp_4w, #NAME "_dp_4w"},                  \
+  {                                                                         \
+    DT, OUT, G9_SCHED_SK, 4, NAME##_sk_4w, #NAME "_sk_4w"                   \
+  }
+
+const KernelEntry kKernels[] = {
+    G9_ENTRY(G9_F16, G9_F16, g9_a16w16_f16),     G9_ENTRY(G9_BF16, G9_BF16, g9_a16w16_bf16),
+    G9_ENTRY(G9_BF8, G9_F16, g9_a8w8_f16out),    G9_ENTRY(G9_BF8, G9_BF16, g9_a8w8_bf16out),
+    G9_ENTRY(G9_FP4, G9_BF16, g9_a4w4_bf16out),  G9_ENTRY(G9_FP4, G9_F16, g9_a4w4_f16out),
+};
+
+const KernelEntry* find_kernel(int dtype, int out, int sched, int waves) {
+  for (const KernelEntry& k : kKernels)
+    if (k.dtype == dtype && k.out == out && k.sched == sched && k.waves == waves) return &k;
+  return nullptr;
+}
+
+// K values per 128-byte stage row.
+int stage_k(int dtype) {
+  switch (dtype) {
+    case G9_F16:
+    case G9_BF16:
+      return 64;
+    case G9_BF8:
+      return 128;
+    case G9_FP4:
+      return 256;
+  }
+  return 0;
+}
+
+constexpr int kNumXcds = 8;
+constexpr int kGroupM = 4;
+constexpr size_t kWsHeader = 256;          // error word + padding
+constexpr size_t kWsTileBytes = 256 * 256 * 4;
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t flags_bytes(long long tiles) { return align256((size_t)tiles * 4); }
+
+std::atomic<unsigned> g_epoch{0};
+
+int cu_count() {
+  static std::once_flag once;
+  static int cus = 0;
+  std::call_once(once, [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cus = n;
+  });
+  return cus;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shared launch path.  Sizes/strides were validated by the caller except the
+// generic checks done here.
+int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
+           void* stream) {
+  if (waves != 4) return G9_ERR_SCHEDULE;
+  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK) return G9_ERR_SCHEDULE;
+  const KernelEntry* k = find_kernel(dtype, out, schedule, waves);
+  if (!k) return G9_ERR_DTYPE;
+  p.tiles_m = (p.M + kTile - 1) / kTile;
+  p.tiles_n = (p.N + kTile - 1) / kTile;
+  p.num_xcds = kNumXcds;
+  p.group_m = kGroupM;
+  const long long tiles = (long long)p.tiles_m * p.tiles_n;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int grid;
+  if (schedule == G9_SCHED_DP) {
+    grid = (int)tiles;
+  } else {
+    const size_t need = kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
+    if (!ws || ws_bytes < need || !aligned(ws, 256)) return G9_ERR_WORKSPACE;
+    char* w = static_cast<char*>(ws);
+    p.err = reinterpret_cast<int*>(w);
+    p.flags = reinterpret_cast<u32*>(w + kWsHeader);
+    p.ws = reinterpret_cast<float*>(w + kWsHeader + flags_bytes(tiles));
+    p.epoch = (g_epoch.fetch_add(1) % 65535u) + 1u;
+    const long long units = tiles * p.ns;
+    int cus = cu_count();
+    if (cus <= 0) return G9_ERR_HIP;
+    grid = (int)(units < cus ? units : cus);
+    p.sk_ctas = grid;
+  }
+  hipLaunchKernelGGL(k->fn, dim3(grid), dim3(kThreads), 0, s, p);
+  return hipGetLastError() == hipSuccess ? G9_OK : G9_ERR_HIP;
+}
+
+int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
+                 const void* c) {
+  if (M <= 0 || N <= 0 || K <= 0) return G9_ERR_SHAPE;
+  if (M > (1 << 30) || N > (1 << 30)) return G9_ERR_SHAPE;
+  const int sk = stage_k(dtype);
+  if (K % sk != 0 || K / sk >= 65536) return G9_ERR_SHAPE;
+  if (stride_cn != 1 || stride_cm < N || !aligned(c, 2)) return G9_ERR_LAYOUT;
+  return G9_OK;
+}
+
+int check_operand(const void* p, int64_t row_stride_bytes, int64_t k_stride, int64_t k_bytes) {
+  if (k_stride != 1) return G9_ERR_LAYOUT;
+  if (!aligned(p, 16) || row_stride_bytes % 16 != 0 || row_stride_bytes < k_bytes) return G9_ERR_LAYOUT;
+  if (row_stride_bytes > (1 << 24)) return G9_ERR_LAYOUT;  // 128 rows x stride must fit 32-bit offsets
+  return G9_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_common(M, N, K, dtype, stride_cm, stride_cn, c);
+  if (st) return st;
+  if ((st = check_operand(a, stride_am * 2, stride_ak, K * 2))) return st;
+  if ((st = check_operand(b, stride_bn * 2, stride_bk, K * 2))) return st;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)(stride_am * 2);
+  p.ldb = (u32)(stride_bn * 2);
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(dtype));
+  return launch(dtype, dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+}
+
+int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_common(M, N, K, G9_BF8, stride_cm, stride_cn, c);
+  if (st) return st;
+  if ((st = check_operand(a, stride_am, stride_ak, K))) return st;
+  if ((st = check_operand(b, stride_bn, stride_bk, K))) return st;
+  if ((a_scale && !aligned(a_scale, 4)) || (b_scale && !aligned(b_scale, 4))) return G9_ERR_LAYOUT;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)stride_am;
+  p.ldb = (u32)stride_bn;
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(G9_BF8));
+  return launch(G9_BF8, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+}
+
+int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_common(M, N, K, G9_FP4, stride_cm, stride_cn, c);
+  if (st) return st;
+  if ((st = check_operand(a, stride_am, stride_ak, K / 2))) return st;
+  if ((st = check_operand(b, stride_bn, stride_bk, K / 2))) return st;
+  if (!a_scales || !b_scales) return G9_ERR_LAYOUT;
+  if (stride_ask != 1 || stride_bsk != 1) return G9_ERR_LAYOUT;
+  if (!aligned(a_scales, 4) || !aligned(b_scales, 4)) return G9_ERR_LAYOUT;
+  if (stride_asm % 4 || stride_bsn % 4 || stride_asm < K / 32 || stride_bsn < K / 32) return G9_ERR_LAYOUT;
+  if (stride_asm > (1 << 24) || stride_bsn > (1 << 24)) return G9_ERR_LAYOUT;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.a_sc = static_cast<const unsigned char*>(a_scales);
+  p.b_sc = static_cast<const unsigned char*>(b_scales);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)stride_am;
+  p.ldb = (u32)stride_bn;
+  p.ldsa = (u32)stride_asm;
+  p.ldsb = (u32)stride_bsn;
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(G9_FP4));
+  return launch(G9_FP4, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+}
+
+size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves) {
+  (void)K;
+  (void)waves;
+  if (schedule != G9_SCHED_SK || M <= 0 || N <= 0 || stage_k(dtype) == 0) return 0;
+  const long long tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
+  return kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
+}
+
+}  // extern "C"
+
+namespace {
+__global__ void zero_words(u32* p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+}  // namespace
+
+extern "C" {
+
+int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace || workspace_bytes < kWsHeader || !aligned(workspace, 256)) return G9_ERR_WORKSPACE;
+  // Header and flags precede the partial tiles; clearing everything up to the
+  // first tile covers both (bounded by the workspace size).
+  size_t words = workspace_bytes / 4;
+  // Flags of at most 2^20 tiles: far beyond any supported shape.
+  const size_t cap = (kWsHeader + flags_bytes(1 << 20)) / 4;
+  if (words > cap) words = cap;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int threads = 256;
+  const int blocks = (int)((words + threads - 1) / threads);
+  hipLaunchKernelGGL(zero_words, dim3(blocks), dim3(threads), 0, s, static_cast<u32*>(workspace), words);
+  return hipGetLastError() == hipSuccess ? G9_OK : G9_ERR_HIP;
+}
+
+int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stream, int* error) {
+  if (!workspace || workspace_bytes < kWsHeader || !error) return G9_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int v = 0;
+  if (hipMemcpyAsync(&v, workspace, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return G9_ERR_HIP;
+  if (hipStreamSynchronize(s) != hipSuccess) return G9_ERR_HIP;
+  *error = v;
+  return G9_OK;
+}
+
+const char* g9_kernel_name(int dtype, int out_dtype, int schedule, int waves) {
+  const KernelEntry* k = find_kernel(dtype, out_dtype, schedule, waves);
+  return k ? k->name : nullptr;
+}
+
+const char* g9_status_string(int status) {
+  switch (status) {
+    case G9_OK:
+      return "ok";
+    case G9_ERR_SHAPE:
+      return "unsupported shape";
+    case G9_ERR_LAYOUT:
+      return "unsupported layout, stride or alignment";
+    case G9_ERR_DTYPE:
+      return "unsupported dtype";
+    case G9_ERR_SCHEDULE:
+      return "unsupported schedule or wave count";
+    case G9_ERR_WORKSPACE:
+      return "stream-K workspace missing or too small";
+    case G9_ERR_HIP:
+      return "HIP launch failed";
+  }
+  return "unknown status";
+}
+
+int g9_streamk_workgroups(void) { return cu_count(); }
+
+int g9_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,582 @@
+// 4-wave (one wave per SIMD) NT GEMM for gfx950: C[M,N] = A[M,K] . B[N,K]^T.
+//
+// One workgroup = 256 threads = 4 waves computes a 256x256 output tile.  The
+// tile is four 128x128 quadrants; wave (wm, wn) owns the 64x64 piece of every
+// quadrant at (wm*64, wn*64), i.e. 2x2 quadrants x 4x4 MFMA 16x16 fragments x
+// 4 fp32 = 256 accumulator registers per lane (they live in AGPRs).
+//
+// K is walked in stages of 128 bytes per operand row: 64 fp16/bf16, 128 bf8 or
+// 256 fp4 values.  A stage is split into four LDS sub-buffers of 128 rows x 128
+// bytes (A rows 0-127 "A0", A rows 128-255 "A1", B rows 0-127 "B0", B rows
+// 128-255 "B1"), each double buffered (two slots), 128 KiB in total.  FP4 adds
+// E8M0 scale sub-buffers of 128 rows x 8 bytes next to them.
+//
+// Per stage every wave runs four "quadrant regions" in the order
+// Q00 (A0 x B0), Q01 (A0 x B1), Q11 (A1 x B1), Q10 (A1 x B0).  Each region
+// issues its MFMAs on operand fragments already in registers, reads the next
+// region's operand set from LDS into registers, and refills, by LDS-DMA, the
+// sub-buffer whose last reads finished in the previous region.  A region
+// starts with `s_waitcnt vmcnt(6 groups) lgkmcnt(0); s_barrier`: the sub-buffer
+// read during a region was requested seven regions earlier, so the DMA latency
+// budget is 1.5 stages (~3000 MFMA cycles) and one barrier per region suffices.
+// The B operand registers alternate roles between even and odd stages, so the
+// loop body covers two stages.
+//
+// LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk slot
+// c ^ ((r >> 1) & 7).  A ds_read_b128 by 16 consecutive lanes (16 rows, one
+// chunk) then touches all 64 banks once.  The LDS-DMA writes each wave's KiB
+// contiguously, so the permutation is applied on the global side: lane i
+// fetches the chunk that belongs in its slot.
+//
+// MFMA operands are swapped (the B fragment is the MFMA's A operand), so lane l
+// ends with C[m0 + l%16][n0 + 4*(l/16) + 0..3]: four consecutive output
+// columns, which the epilogue writes to LDS as one 8-byte store and then streams
+// out as coalesced 16-byte row chunks.
+#pragma once
+
+#include <utility>
+
+#include "g9_common.hpp"
+
+namespace g9 {
+
+enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3 };
+enum : int { OUT_F16 = 0, OUT_BF16 = 1 };
+
+struct GemmParams {
+  const char* a;              // A: M rows of K-contiguous elements, lda bytes apart
+  const char* b;              // B: N rows of K-contiguous elements, ldb bytes apart
+  char* c;                    // C: M x N 16-bit values, row stride ldc elements
+  const unsigned char* a_sc;  // FP4 only: E8M0 scales, M rows of K/32 bytes, ldsa apart
+  const unsigned char* b_sc;  // FP4 only: N rows
+  const float* a_scale;       // BF8 only: per-tensor fp32 scales on the device (nullable)
+  const float* b_scale;
+  int M, N, K;                // K in elements
+  u32 lda, ldb;               // operand row strides in bytes
+  u32 ldsa, ldsb;             // scale row strides in bytes
+  long long ldc;              // C row stride in elements
+  int ns;                     // K stages (K * bits / 1024)
+  int tiles_m, tiles_n;
+  int num_xcds, group_m;
+  // stream-K
+  float* ws;                  // fp32 partial tiles (256 KiB per tile)
+  u32* flags;                 // one flag per tile: (epoch << 16) | stages done
+  u32 epoch;
+  int* err;                   // set to 1 when a flag wait times out
+  int sk_ctas;                // persistent workgroups
+};
+
+constexpr int kTile = 256;
+constexpr int kThreads = 256;
+constexpr int kRowBytes = 128;              // bytes of one operand row per stage
+constexpr int kSubBytes = 128 * kRowBytes;  // one sub-buffer (16 KiB)
+constexpr int kScaleBase = 131072;          // FP4 scale sub-buffers (8 x 1 KiB)
+constexpr int kStageRow = 528;              // epilogue staging row pitch (bytes)
+constexpr int kLdsBytes4w = 139264;         // 128 KiB operands + 8 KiB scales
+static_assert(kTile * kStageRow <= kLdsBytes4w, "staging must fit");
+
+// Operand fragment of one 16-row slice for one stage: 32 bytes per lane, plus
+// (FP4) the lane's 8 raw scale bytes of the stage.
+struct Frag {
+  u32x4 c[2];
+  u32x2 sc;
+};
+
+template <Op OP>
+struct OpInfo {
+  static constexpr bool kScaled = OP == Op::FP4;
+  static constexpr int kSub = OP == Op::BF8 ? 1 : 2;  // MFMAs per fragment pair per stage
+  static constexpr int kDmaPerRegion = kScaled ? 5 : 4;
+  static constexpr int kMfmaPerRegion = 16 * kSub;
+  // The two 16-byte chunks (of the row's eight) lane group g reads per stage.
+  static G9_DEV int chunk(int e, int g) { return OP == Op::BF8 ? 2 * g + e : 4 * e + g; }
+};
+
+// LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
+constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s) * kSubBytes; }
+constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; }
+
+// One MFMA of step H of the stage on a (B fragment, A fragment) pair, written
+// as inline assembly with the accumulator tied in place ("+a").  The compiler
+// selects an untied MFMA form for the builtins and then renames every
+// accumulator chain across the 256 AGPRs, which costs hundreds of AGPR copies
+// per loop iteration; the tied form keeps each chain in its registers.  The
+// hazard recognizer does not see through inline assembly, so the callers
+// insert the MFMA-to-VALU wait states themselves (see mfma_drain) and never
+// feed an MFMA from a VALU result written within a few cycles.
+// `sc` holds the lane's two E8M0 scales (FP4 only).
+template <Op OP, int H>
+G9_DEV void mma(f32x4& acc, const Frag& bx, const Frag& ay, u32 scx, u32 scy) {
+  if constexpr (OP == Op::F16) {
+    asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[H]), "v"(ay.c[H]));
+  } else if constexpr (OP == Op::BF16) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[H]), "v"(ay.c[H]));
+  } else if constexpr (OP == Op::BF8) {
+    // e5m2 x e5m2 (format code 1), 32 bytes per lane; no block scales (the
+    // per-tensor scales are applied in the epilogue).
+    const i32x8 x = __builtin_bit_cast(i32x8, __builtin_shufflevector(bx.c[0], bx.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    const i32x8 y = __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[0], ay.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
+  } else {
+    // e2m1 x e2m1 (format code 4), 16 bytes per lane.  Byte H of the scale
+    // registers is scale group 4H+g of the lane's row (op_sel picks it).
+    if constexpr (H == 0)
+      asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"
+          : "+a"(acc)
+          : "v"(bx.c[0]), "v"(ay.c[0]), "v"(scx), "v"(scy));
+    else
+      asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"
+          : "+a"(acc)
+          : "v"(bx.c[1]), "v"(ay.c[1]), "v"(scx), "v"(scy));
+  }
+}
+
+// Wait states between the last inline-assembly MFMA writing an accumulator and
+// the first VALU/memory access to it (the longest gfx950 MFMA here has 8
+// passes; 3 x s_nop 7 covers it with margin).
+G9_DEV void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Where, inside a region of NM MFMAs, the other instructions are issued (they
+// go right after MFMA number k).  The eight 16-byte LDS reads come first so the
+// region-closing lgkmcnt(0) finds them complete; the DMAs are spread evenly so
+// the four waves of a CU keep the texture-address pipe at its issue rate.
+template <Op OP>
+struct Slots {
+  static constexpr int NM = OpInfo<OP>::kMfmaPerRegion;
+  static constexpr int read16(int k) {  // 16-byte read number issued after MFMA k, or -1
+    if constexpr (OP == Op::BF8) return k < 8 ? k : -1;
+    else return (k % 2 == 0 && k < 16) ? k / 2 : -1;
+  }
+  static constexpr int read8(int k) {  // FP4 scale-row read number, or -1
+    return (OP == Op::FP4 && k % 4 == 1 && k < 16) ? k / 4 : -1;
+  }
+  static constexpr int dma16(int k) {  // 16-byte DMA number, or -1
+    if constexpr (OP == Op::BF8) return k % 4 == 1 ? k / 4 : -1;
+    else return k % 8 == 1 ? k / 8 : -1;
+  }
+  static constexpr bool dma4(int k) { return OP == Op::FP4 && k == 5; }
+};
+
+// Keeps a value in a register the compiler cannot see through, so constant
+// parts of LDS addresses stay in the instruction's offset field.
+G9_DEV u32 opaque(u32 x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Per-workgroup pipeline state: buffer resources, per-lane DMA offsets and LDS
+// read bases.  One instance per output tile (rebuilt per stream-K segment).
+template <Op OP>
+struct Pipe {
+  using I = OpInfo<OP>;
+  rsrc_t rA[2], rB[2], rZ;  // operand half-tiles; rZ has no valid bytes (reads 0)
+  rsrc_t rSA[2], rSB[2];    // FP4 scale half-tiles
+  u32 vA[4], vB[4];         // DMA offsets of the wave's four 1-KiB runs
+  u32 vSA, vSB;             // FP4 scale DMA offsets
+  u32 bA[2], bB[2];         // LDS read bases of the lane's two chunks (A at 0, B at 64 KiB)
+  u32 bSA, bSB;             // FP4 LDS read bases of the lane's scale row (at 128 KiB)
+  u32 sel;                  // FP4 scale byte selector
+  u32 lds0;                 // LDS address of the shared buffer
+  int wave;
+  int s_end;                // first stage not to load
+
+  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int end) {
+    s_end = end;
+    lds0 = (u32)(uintptr_t)to_lds(smem);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r16 = lane & 15;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ra = tm * kTile + h * 128, rb = tn * kTile + h * 128;
+      const int va = min(max(p.M - ra, 0), 128), vb = min(max(p.N - rb, 0), 128);
+      rA[h] = make_rsrc(p.a + (size_t)ra * p.lda, (u32)va * p.lda);
+      rB[h] = make_rsrc(p.b + (size_t)rb * p.ldb, (u32)vb * p.ldb);
+      if constexpr (I::kScaled) {
+        rSA[h] = make_rsrc(p.a_sc + (size_t)ra * p.ldsa, (u32)va * p.ldsa);
+        rSB[h] = make_rsrc(p.b_sc + (size_t)rb * p.ldsb, (u32)vb * p.ldsb);
+      }
+    }
+    rZ = make_rsrc(p.a, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 32 * wave + 8 * j + (lane >> 3);
+      const int ch = (lane & 7) ^ (4 * (j & 1) + (lane >> 4));
+      vA[j] = (u32)row * p.lda + ch * 16;
+      vB[j] = (u32)row * p.ldb + ch * 16;
+    }
+    const int sw = r16 >> 1;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int slot = I::chunk(e, g) ^ sw;
+      bA[e] = opaque(lds0 + (u32)(wm * 64 + r16) * kRowBytes + slot * 16);
+      bB[e] = opaque(lds0 + 65536u + (u32)(wn * 64 + r16) * kRowBytes + slot * 16);
+    }
+    if constexpr (I::kScaled) {
+      const int row = 32 * wave + (lane >> 1);
+      vSA = (u32)row * p.ldsa + (lane & 1) * 4;
+      vSB = (u32)row * p.ldsb + (lane & 1) * 4;
+      bSA = opaque(lds0 + kScaleBase + (u32)(wm * 64 + r16) * 8);
+      bSB = opaque(lds0 + kScaleBase + (u32)(wn * 64 + r16) * 8);
+      sel = (u32)g | ((u32)(4 + g) << 8) | 0x0c0c0000u;
+    } else {
+      sel = 0;
+    }
+  }
+
+  G9_DEV rsrc_t src(int X, bool live) const { return live ? (X < 2 ? rA[X & 1] : rB[X & 1]) : rZ; }
+  G9_DEV rsrc_t src_sc(int X, bool live) const { return live ? (X < 2 ? rSA[X & 1] : rSB[X & 1]) : rZ; }
+
+  // 16-byte DMA number J (rows 8J..8J+7 of the wave's 32) of sub-buffer X.
+  template <int X, int SLOT, int J>
+  G9_DEV void dma_rows(rsrc_t r, u32 soff) const {
+    const u32 dst = lds0 + sub_off(X, SLOT) + (u32)wave * 4096u + J * 1024;
+    dma16(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
+  }
+  template <int X, int SLOT>
+  G9_DEV void dma_scales(rsrc_t r, u32 soff) const {
+    const u32 dst = lds0 + scale_off(X, SLOT) + (u32)wave * 256u;
+    dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
+  }
+
+  // 16-byte LDS read number R (fragment R/2, chunk R%2) of sub-buffer X.
+  template <int X, int SLOT, int R>
+  G9_DEV void read_chunk(Frag (&f)[4]) const {
+    constexpr int region = X < 2 ? 0 : 65536;
+    constexpr int imm = sub_off(X, SLOT) - region + (R / 2) * 2048;
+    const u32 base = X < 2 ? bA[R % 2] : bB[R % 2];
+    f[R / 2].c[R % 2] = *(const G9_LDS u32x4*)(uintptr_t)(base + imm);
+  }
+  template <int X, int SLOT, int F>
+  G9_DEV void read_scales(Frag (&f)[4]) const {
+    constexpr int imm = scale_off(X, SLOT) - kScaleBase + F * 128;
+    const u32 base = X < 2 ? bSA : bSB;
+    f[F].sc = *(const G9_LDS u32x2*)(uintptr_t)(base + imm);
+  }
+
+  // Whole-set variants for the prologue.
+  template <int X, int SLOT>
+  G9_DEV void issue(int stage) const {
+    const bool live = stage < s_end;
+    const rsrc_t r = src(X, live);
+    const u32 soff = (u32)stage * kRowBytes;
+    dma_rows<X, SLOT, 0>(r, soff);
+    dma_rows<X, SLOT, 1>(r, soff);
+    dma_rows<X, SLOT, 2>(r, soff);
+    dma_rows<X, SLOT, 3>(r, soff);
+    if constexpr (I::kScaled) dma_scales<X, SLOT>(src_sc(X, live), (u32)stage * 8);
+  }
+  template <int X, int SLOT>
+  G9_DEV void load(Frag (&f)[4]) const {
+    [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
+        std::make_integer_sequence<int, 8>{});
+    if constexpr (I::kScaled) {
+      [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SLOT, F>(f), ...); }(
+          std::make_integer_sequence<int, 4>{});
+    }
+  }
+};
+
+// Region prologue: all but the last six DMA groups landed and the wave's own
+// LDS reads complete, then the workgroup barrier.  The leading scheduling
+// fence keeps the wait at the region boundary.
+template <Op OP>
+G9_DEV void region_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  waitcnt<6 * OpInfo<OP>::kDmaPerRegion, 0>();
+  barrier();
+}
+
+// Slot K of a region: MFMA number K (step-major: step, A fragment, B
+// fragment), then whatever the slot table puts after it, then a fence that
+// lets only scalar/vector ALU work move across.
+template <Op OP, int RX, int RSLOT, int DX, int DSLOT, int K>
+G9_DEV void region_slot(const Pipe<OP>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, f32x4 (&acc)[4][4],
+                        const Frag (&bx)[4], const Frag (&ay)[4], const u32 (&scx)[4], const u32 (&scy)[4],
+                        Frag (&nxt)[4]) {
+  using S = Slots<OP>;
+  constexpr int h = K / 16, i = (K / 4) % 4, j = K % 4;
+  mma<OP, h>(acc[i][j], bx[j], ay[i], scx[j], scy[i]);
+  if constexpr (S::read16(K) >= 0) P.template read_chunk<RX, RSLOT, S::read16(K)>(nxt);
+  if constexpr (S::read8(K) >= 0) P.template read_scales<RX, RSLOT, S::read8(K)>(nxt);
+  if constexpr (S::dma16(K) >= 0) P.template dma_rows<DX, DSLOT, S::dma16(K)>(r, soff);
+  if constexpr (S::dma4(K)) P.template dma_scales<DX, DSLOT>(rs, soff_sc);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One quadrant region: MFMAs of (bx, ay) into acc, LDS reads of sub-buffer
+// RX/RSLOT into nxt, DMA of stage `ds` into sub-buffer DX/DSLOT.
+template <Op OP, int RX, int RSLOT, int DX, int DSLOT>
+G9_DEV void region(const Pipe<OP>& P, int ds, f32x4 (&acc)[4][4], const Frag (&bx)[4], const Frag (&ay)[4],
+                   Frag (&nxt)[4]) {
+  region_sync<OP>();
+  const bool live = ds < P.s_end;
+  const rsrc_t r = P.src(DX, live);
+  rsrc_t rs = r;
+  if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
+  const u32 soff = (u32)ds * kRowBytes, soff_sc = (u32)ds * 8;
+  // FP4: gather each fragment's two scale bytes (VALU) before the first MFMA,
+  // with wait states between the last write and the MFMA reads.
+  u32 scx[4] = {0, 0, 0, 0}, scy[4] = {0, 0, 0, 0};
+  if constexpr (OpInfo<OP>::kScaled) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      scx[f] = __builtin_amdgcn_perm(bx[f].sc.y, bx[f].sc.x, P.sel);
+      scy[f] = __builtin_amdgcn_perm(ay[f].sc.y, ay[f].sc.x, P.sel);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 4" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    (region_slot<OP, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, scx, scy, nxt), ...);
+  }(std::make_integer_sequence<int, Slots<OP>::NM>{});
+}
+
+// Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
+// they are consumed the next stage's B0 fragments go to y as well.
+template <Op OP>
+G9_DEV void stage_even(const Pipe<OP>& P, int s, f32x4 (&acc)[2][2][4][4], Frag (&at)[4], Frag (&ab)[4],
+                       Frag (&x)[4], Frag (&y)[4]) {
+  region<OP, 3, 0, 2, 0>(P, s + 2, acc[0][0], x, at, y);
+  region<OP, 1, 0, 3, 0>(P, s + 2, acc[0][1], y, at, ab);
+  region<OP, 0, 1, 1, 0>(P, s + 2, acc[1][1], y, ab, at);
+  region<OP, 2, 1, 0, 1>(P, s + 3, acc[1][0], x, ab, y);
+}
+
+// Odd stage (slot 1): B0 fragments in y; B1 fragments go to x, then the next
+// stage's B0 fragments.
+template <Op OP>
+G9_DEV void stage_odd(const Pipe<OP>& P, int s, f32x4 (&acc)[2][2][4][4], Frag (&at)[4], Frag (&ab)[4],
+                      Frag (&x)[4], Frag (&y)[4]) {
+  region<OP, 3, 1, 2, 1>(P, s + 2, acc[0][0], y, at, x);
+  region<OP, 1, 1, 3, 1>(P, s + 2, acc[0][1], x, at, ab);
+  region<OP, 0, 0, 1, 1>(P, s + 2, acc[1][1], x, ab, at);
+  region<OP, 2, 0, 0, 0>(P, s + 3, acc[1][0], y, ab, x);
+}
+
+// Accumulates stages [s0, s1) of tile (tm, tn) into acc.  Leaves every DMA
+// complete and the workgroup synchronised, so LDS is free on return.
+template <Op OP>
+G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1,
+                     f32x4 (&acc)[2][2][4][4]) {
+  using I = OpInfo<OP>;
+  Pipe<OP> P;
+  P.init(p, smem, tm, tn, s1);
+  // DMA stream order: per stage A0, B0, B1, A1.  Stage s lives in slot (s-s0)&1.
+  P.template issue<0, 0>(s0);
+  P.template issue<2, 0>(s0);
+  P.template issue<3, 0>(s0);
+  P.template issue<1, 0>(s0);
+  P.template issue<0, 1>(s0 + 1);
+  P.template issue<2, 1>(s0 + 1);
+  P.template issue<3, 1>(s0 + 1);
+  P.template issue<1, 1>(s0 + 1);
+  // A0(s0) and B0(s0) landed: read them, then (once every wave has) refill
+  // A0 slot 0 with stage s0+2.
+  waitcnt<6 * I::kDmaPerRegion, 0>();
+  barrier();
+  Frag at[4], ab[4], x[4], y[4];
+  P.template load<0, 0>(at);
+  P.template load<2, 0>(x);
+  waitcnt<6 * I::kDmaPerRegion, 0>();
+  barrier();
+  P.template issue<0, 0>(s0 + 2);
+  // The accumulators were just written by VALU (zeroing or a partial tile):
+  // wait states before the first MFMA reads them.
+  mfma_drain();
+  // Two stages per iteration (the B registers swap roles between them), then
+  // a peeled even stage when the count is odd.
+  int s = s0;
+  const int pairs = (s1 - s0) >> 1;
+  for (int it = 0; it < pairs; ++it, s += 2) {
+    stage_even(P, s, acc, at, ab, x, y);
+    stage_odd(P, s + 1, acc, at, ab, x, y);
+  }
+  if ((s1 - s0) & 1) stage_even(P, s, acc, at, ab, x, y);
+  mfma_drain();
+  waitcnt<0, 0>();
+  barrier();
+}
+
+G9_DEV void zero_acc(f32x4 (&acc)[2][2][4][4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[q >> 1][q & 1][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Converts the tile to 16-bit (after multiplying by `scale`), stages it in LDS
+// and writes it to C with coalesced 16-byte row chunks, masking rows >= M and
+// columns >= N.  LDS must be free on entry; it is free again on return.
+template <int OUT>
+G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, f32x4 (&acc)[2][2][4][4],
+                       float scale) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int qm = 0; qm < 2; ++qm)
+#pragma unroll
+    for (int qn = 0; qn < 2; ++qn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = qm * 128 + wm * 64 + i * 16 + r16;
+          const int n = qn * 128 + wn * 64 + j * 16 + 4 * g;
+          const f32x4 v = acc[qm][qn][i][j] * scale;
+          const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
+          lds_write8(smem + m * kStageRow + n * 2, h);
+        }
+  waitcnt<0, 0>();
+  barrier();
+  const int ch = tid & 31;
+  const int row0 = tm * kTile, col = tn * kTile + ch * 8;
+  char* cbase = p.c + (size_t)col * 2;
+#pragma unroll 4
+  for (int pass = 0; pass < 32; ++pass) {
+    const int r = pass * 8 + (tid >> 5);
+    const u32x4 d = lds_read16(smem + r * kStageRow + ch * 16);
+    const int m = row0 + r;
+    if (m < p.M) {
+      char* dst = cbase + (size_t)m * p.ldc * 2;
+      if (col + 8 <= p.N && ((uintptr_t)dst & 15) == 0) {
+        *reinterpret_cast<u32x4*>(dst) = d;
+      } else {
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&d);
+        for (int e = 0; e < 8; ++e)
+          if (col + e < p.N) reinterpret_cast<uint16_t*>(dst)[e] = hv[e];
+      }
+    }
+  }
+  barrier();
+}
+
+template <Op OP>
+G9_DEV float epilogue_scale(const GemmParams& p) {
+  if constexpr (OP == Op::BF8) {
+    float s = 1.f;
+    if (p.a_scale) s *= *p.a_scale;
+    if (p.b_scale) s *= *p.b_scale;
+    return s;
+  } else {
+    return 1.f;
+  }
+}
+
+// Data-parallel schedule: one workgroup per 256x256 output tile.
+template <Op OP, int OUT>
+G9_DEV void gemm_dp_4w(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes4w];
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, tm, tn);
+  f32x4 acc[2][2][4][4];
+  zero_acc(acc);
+  mainloop<OP>(p, smem, tm, tn, 0, p.ns, acc);
+  store_tile<OUT>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K schedule.
+//
+// The (tile, stage) space is linearised tile-major and cut into `sk_ctas`
+// contiguous ranges, one per persistent workgroup.  A tile whose stages span
+// several ranges is finished by a K-ordered chain: the owner of stages
+// [sb, se) with sb > 0 waits for the tile's flag to read (epoch, sb), loads the
+// predecessor's fp32 partial as its initial accumulator and continues, so
+// every output element sees exactly the MFMA sequence of the data-parallel
+// kernel and the result is bit-identical to it.  Each workgroup walks its
+// range from the last tile backwards, so the prefix it owes a successor is
+// produced first and the suffix it inherits is consumed last.
+// ---------------------------------------------------------------------------
+constexpr u32 kSpinLimit = 1u << 26;
+
+G9_DEV int ws_index(int wave, int q, int i, int j, int lane) {
+  return ((wave * 64 + (q * 4 + i) * 4 + j) * 64 + lane);
+}
+
+G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
+  u32 spins = 0;
+  while (__hip_atomic_load(p.flags + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++spins > kSpinLimit) {
+      __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+template <Op OP, int OUT>
+G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se) {
+  int tm, tn;
+  tile_coords(tile, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, 1, p.group_m, tm, tn);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  f32x4* ws = reinterpret_cast<f32x4*>(p.ws) + (size_t)tile * (kTile * kTile / 4);
+  f32x4 acc[2][2][4][4];
+  if (sb == 0) {
+    zero_acc(acc);
+  } else {
+    wait_flag(p, tile, (p.epoch << 16) | (u32)sb);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[q >> 1][q & 1][i][j] = ws[ws_index(wave, q, i, j, lane)];
+  }
+  mainloop<OP>(p, smem, tm, tn, sb, se, acc);
+  if (se == p.ns) {
+    store_tile<OUT>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+    if (sb != 0 && tid == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ws[ws_index(wave, q, i, j, lane)] = acc[q >> 1][q & 1][i][j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    barrier();
+    if (tid == 0)
+      __hip_atomic_store(p.flags + tile, (p.epoch << 16) | (u32)se, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <Op OP, int OUT>
+G9_DEV void gemm_sk_4w(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes4w];
+  const int G = p.sk_ctas;
+  // Workgroup ids are dispatched round-robin over the XCDs; give each XCD a
+  // contiguous run of ranges so chained neighbours share an L2.
+  int cta = blockIdx.x;
+  {
+    int cm, cn;
+    tile_coords(cta, G, G, 1, p.num_xcds, 1, cm, cn);
+    cta = cm;
+  }
+  const long long ipt = p.ns;
+  const long long total = (long long)p.tiles_m * p.tiles_n * ipt;
+  const long long base = total / G, rem = total % G;
+  const long long u0 = cta * base + min((long long)cta, rem);
+  long long u1 = u0 + base + (cta < rem ? 1 : 0);
+  while (u1 > u0) {
+    const int tile = (int)((u1 - 1) / ipt);
+    const long long t0 = (long long)tile * ipt;
+    const int sb = (int)(max(u0, t0) - t0);
+    const int se = (int)(u1 - t0);
+    sk_segment<OP, OUT>(p, smem, tile, sb, se);
+    u1 = t0 + sb;
+  }
+}
+
+}  // namespace g9

@@ -1,0 +1,220 @@
+"""Tensor-level launch helpers shared by the per-dtype ``matmul`` wrappers.
+
+Every wrapper ends here: tensors are checked (device, dtype, layout), turned
+into raw pointers/strides and passed to the C ABI on the current HIP stream of
+the operands' device.  The launch is asynchronous, as in the reference.
+
+Layout handling mirrors the reference's contract: the kernels want both
+operands K-contiguous ("NT").  A B operand given as a (K, N) view of an (N, K)
+buffer (the reference benches' ``b = randn(N, K).T``) is used in place; any
+other layout is first repacked to (N, K) contiguous on the device, which is
+what ``kernels/gemm/inter_wave/a8w8/matmul_kernel.py:385`` does unconditionally.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from .. import _lib
+
+_DTYPE_CODE = {torch.float16: _lib.G9_F16, torch.bfloat16: _lib.G9_BF16}
+_OUT_CODE = {torch.float16: _lib.G9_F16, torch.bfloat16: _lib.G9_BF16}
+
+# Stage depth in K elements per operand type (K must be a multiple).
+STAGE_K = {_lib.G9_F16: 64, _lib.G9_BF16: 64, _lib.G9_BF8: 128, _lib.G9_FP4: 256}
+
+
+def _schedule_code(schedule) -> int:
+    if isinstance(schedule, int):
+        return schedule
+    try:
+        return _lib.SCHEDULES[str(schedule).lower()]
+    except KeyError:
+        raise ValueError(f"unknown schedule {schedule!r} (expected 'dp' or 'streamk')") from None
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError(f"gfx950 GEMM operands must be GPU tensors, got one on {t.device}")
+        if t.device != dev:
+            raise ValueError(f"operands on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
+    """Returns a (K, N) view whose K stride is 1 (an (N, K) row-major buffer)."""
+    if b_kn.stride(0) == 1 and b_kn.stride(1) >= b_kn.shape[0]:
+        return b_kn
+    return b_kn.t().contiguous().t()
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    """Row-major with unit inner stride and 16-byte aligned rows."""
+    es = t.element_size()
+    return (
+        t.dim() == 2
+        and t.stride(1) == 1
+        and t.data_ptr() % 16 == 0
+        and (t.stride(0) * es) % 16 == 0
+        and t.stride(0) >= t.shape[1]
+    )
+
+
+class _Workspaces:
+    """Per-device stream-K workspace (fp32 partial tiles + flags), grown on
+    demand and zeroed once.  Launches that reuse it are ordered on one stream;
+    launches on different streams must not overlap."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def get(self, dev: torch.device, nbytes: int, stream: int) -> tuple[int, int]:
+        if nbytes == 0:
+            return 0, 0
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        with self._lock:
+            ws = self._ws.get(idx)
+            if ws is None or ws.numel() < nbytes:
+                ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+                _lib.check(_lib.load().g9_workspace_init(ws.data_ptr(), ws.numel(), stream), "workspace init")
+                self._ws[idx] = ws
+        return ws.data_ptr(), ws.numel()
+
+    def error(self, dev: torch.device) -> int:
+        """Synchronises the device's current stream and returns the error word
+        (1 = a stream-K flag wait timed out)."""
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        ws = self._ws.get(idx)
+        if ws is None:
+            return 0
+        out = _lib.ctypes.c_int(0)
+        _lib.check(_lib.load().g9_workspace_error(ws.data_ptr(), ws.numel(), _stream(dev), _lib.ctypes.byref(out)),
+                   "workspace error query")
+        return out.value
+
+
+WORKSPACES = _Workspaces()
+
+
+def _workspace(lib, dt: int, M: int, N: int, K: int, sched: int, waves: int, dev, stream) -> tuple[int, int]:
+    need = lib.g9_workspace_size(dt, M, N, K, sched, waves)
+    return WORKSPACES.get(dev, need, stream)
+
+
+def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedule="dp", waves: int = 4):
+    """C = A @ B with A (M, K), B a (K, N) view, C (M, N); fp16 or bf16."""
+    lib = _lib.load()
+    dev = _require_device(a, b_kn, c)
+    if a.dtype not in _DTYPE_CODE or b_kn.dtype != a.dtype or c.dtype != a.dtype:
+        raise ValueError(f"a16w16 needs matching fp16/bf16 a, b, c; got {a.dtype}, {b_kn.dtype}, {c.dtype}")
+    M, K = a.shape
+    N = b_kn.shape[1]
+    if c.shape != (M, N):
+        raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
+    if not _rows_ok(a):
+        a = a.contiguous()
+    b_kn = _k_major(b_kn)
+    dt = _DTYPE_CODE[a.dtype]
+    sched = _schedule_code(schedule)
+    stream = _stream(dev)
+    ws, ws_bytes = _workspace(lib, dt, M, N, K, sched, waves, dev, stream)
+    rc = lib.g9_gemm_a16w16(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
+                            a.stride(0), a.stride(1), b_kn.stride(0), b_kn.stride(1),
+                            c.stride(0), c.stride(1), dt, sched, waves, ws, ws_bytes, stream)
+    _lib.check(rc, "g9_gemm_a16w16")
+    return c
+
+
+def _scale_tensor(s, dev) -> torch.Tensor | None:
+    if s is None:
+        return None
+    if not isinstance(s, torch.Tensor):
+        return torch.tensor([float(s)], dtype=torch.float32, device=dev)
+    if s.numel() != 1:
+        raise ValueError("a8w8 scales are per-tensor: one fp32 value each")
+    return s.detach().reshape(1).to(device=dev, dtype=torch.float32)
+
+
+def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=None, b_scale=None,
+              schedule="dp", waves: int = 4):
+    """C = (A @ B) * a_scale * b_scale with BF8 (e5m2) A (M, K), B a (K, N) view."""
+    lib = _lib.load()
+    dev = _require_device(a, b_kn, c)
+    if a.dtype != torch.float8_e5m2 or b_kn.dtype != torch.float8_e5m2:
+        raise ValueError(f"a8w8 needs float8_e5m2 operands; got {a.dtype}, {b_kn.dtype}")
+    if c.dtype not in _OUT_CODE:
+        raise ValueError(f"a8w8 output must be fp16 or bf16, got {c.dtype}")
+    M, K = a.shape
+    N = b_kn.shape[1]
+    if c.shape != (M, N):
+        raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
+    if not _rows_ok(a):
+        a = a.contiguous()
+    b_kn = _k_major(b_kn)
+    sa = _scale_tensor(a_scale, dev)
+    sb = _scale_tensor(b_scale, dev)
+    sched = _schedule_code(schedule)
+    stream = _stream(dev)
+    ws, ws_bytes = _workspace(lib, _lib.G9_BF8, M, N, K, sched, waves, dev, stream)
+    rc = lib.g9_gemm_a8w8(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
+                          a.stride(0), a.stride(1), b_kn.stride(0), b_kn.stride(1),
+                          c.stride(0), c.stride(1),
+                          sa.data_ptr() if sa is not None else None,
+                          sb.data_ptr() if sb is not None else None,
+                          _OUT_CODE[c.dtype], sched, waves, ws, ws_bytes, stream)
+    _lib.check(rc, "g9_gemm_a8w8")
+    return c
+
+
+def _scales_ok(s: torch.Tensor) -> bool:
+    return s.stride(1) == 1 and s.stride(0) % 4 == 0 and s.stride(0) >= s.shape[1] and s.data_ptr() % 4 == 0
+
+
+def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales: torch.Tensor, c: torch.Tensor,
+              *, schedule="dp", waves: int = 4):
+    """C = dequant(A) @ dequant(B)^T with packed MXFP4 A (M, K/2), B (N, K/2)
+    and E8M0 scales (M, K/32), (N, K/32)."""
+    lib = _lib.load()
+    dev = _require_device(a, b, a_scales, b_scales, c)
+    for name, t in (("a", a), ("b", b), ("a_scales", a_scales), ("b_scales", b_scales)):
+        if t.dtype != torch.uint8 or t.dim() != 2:
+            raise ValueError(f"a4w4 {name} must be a 2-D uint8 tensor, got {t.dtype} {tuple(t.shape)}")
+    if c.dtype not in _OUT_CODE:
+        raise ValueError(f"a4w4 output must be bf16 or fp16, got {c.dtype}")
+    M, Kp = a.shape
+    N = b.shape[0]
+    K = 2 * Kp
+    if b.shape[1] != Kp:
+        raise ValueError(f"a and b packed K differ: {Kp} vs {b.shape[1]}")
+    if a_scales.shape != (M, K // 32) or b_scales.shape != (N, K // 32):
+        raise ValueError(f"scales must be ({M}, {K // 32}) and ({N}, {K // 32}); got "
+                         f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
+    if c.shape != (M, N):
+        raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
+    if not _rows_ok(a):
+        a = a.contiguous()
+    if not _rows_ok(b):
+        b = b.contiguous()
+    if not _scales_ok(a_scales):
+        a_scales = a_scales.contiguous()
+    if not _scales_ok(b_scales):
+        b_scales = b_scales.contiguous()
+    sched = _schedule_code(schedule)
+    stream = _stream(dev)
+    ws, ws_bytes = _workspace(lib, _lib.G9_FP4, M, N, K, sched, waves, dev, stream)
+    rc = lib.g9_gemm_a4w4(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(),
+                          M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+                          c.stride(0), c.stride(1), a_scales.stride(0), a_scales.stride(1),
+                          b_scales.stride(0), b_scales.stride(1), _OUT_CODE[c.dtype], sched, waves,
+                          ws, ws_bytes, stream)
+    _lib.check(rc, "g9_gemm_a4w4")
+    return c

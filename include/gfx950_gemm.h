@@ -1,0 +1,133 @@
+/*
+ * gfx950_gemm.h -- C ABI of the MI355X (gfx950) NT GEMM library.
+ *
+ * C[M,N] = A[M,K] . B[K,N] where both operands are K-contiguous in memory
+ * ("NT": A is M rows of K values, B is N rows of K values).  Three operand
+ * types: FP16/BF16 (a16w16), BF8 = fp8 e5m2 with optional per-tensor fp32
+ * scales (a8w8), and MXFP4 = e2m1 packed two per byte with one E8M0 scale per
+ * 32 K-values (a4w4).  Two tile schedules: data-parallel (one 256x256 tile per
+ * workgroup) and stream-K (persistent workgroups over (tile, K-stage) work with
+ * a K-ordered fp32 fixup; bit-identical to data-parallel).
+ *
+ * Every entry point takes raw device pointers, sizes and strides in ELEMENTS
+ * (bytes for the uint8 MXFP4 operands and scales), launches asynchronously on
+ * `stream` (a hipStream_t; NULL = default stream) and returns a status code.
+ * Nothing is synchronised and nothing is allocated: the stream-K workspace is
+ * owned by the caller (size from g9_workspace_size, zeroed once with
+ * g9_workspace_init before first use, and not shared by launches that may run
+ * concurrently).
+ *
+ * The per-dtype entry points replace the launch wrappers of the reference's
+ * Gluon kernels (argument order a, b, c, M, N, K, stride_am, stride_ak,
+ * stride_bk, stride_bn, stride_cm, stride_cn as in their kernel launches).
+ */
+#ifndef GFX950_GEMM_H
+#define GFX950_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+  G9_OK = 0,
+  G9_ERR_SHAPE = 1,     /* non-positive or unsupported M/N/K (K must be a multiple of the K stage) */
+  G9_ERR_LAYOUT = 2,    /* K stride != 1, N stride of C != 1, operand rows not 16-byte aligned */
+  G9_ERR_DTYPE = 3,     /* unsupported element / output type */
+  G9_ERR_SCHEDULE = 4,  /* unknown schedule or wave count */
+  G9_ERR_WORKSPACE = 5, /* stream-K workspace missing or too small */
+  G9_ERR_HIP = 6        /* the HIP runtime rejected the launch */
+};
+
+/* Element / output types. */
+enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3 };
+
+/* Tile schedules. */
+enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1 };
+
+/*
+ * a16w16: FP16 or BF16 (`dtype` = G9_F16 / G9_BF16) in and out, fp32 accumulate.
+ * Replaces the launch in kernels/gemm/intra_wave/a16w16/v9_beyond_hotloop/matmul_kernel.py:390-424
+ * (4-wave, `waves` = 4) and the missing 8-wave kernel bound by
+ * kernels/gemm/inter_wave/a16w16/bench.py:48 (`waves` = 8).
+ * K must be a multiple of 64.
+ */
+int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * a8w8: BF8 (fp8 e5m2) in, fp32 accumulate, C = (A.B) * a_scale[0] * b_scale[0]
+ * written as `out_dtype` (G9_F16, the reference default, or G9_BF16).  The scale
+ * pointers are device fp32 scalars; NULL means 1.0.
+ * Replaces kernels/gemm/intra_wave/a8w8/matmul_kernel.py:437-470 (4-wave) and
+ * kernels/gemm/inter_wave/a8w8/matmul_kernel.py:343-388 (8-wave).
+ * K must be a multiple of 128.
+ */
+int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * a4w4: MXFP4.  a is M x K/2 bytes, b is N x K/2 bytes (two e2m1 values per
+ * byte, low nibble = even k); a_scales is M x K/32 and b_scales N x K/32 E8M0
+ * bytes (2^(x-127)).  K is the logical (unpacked) depth, a multiple of 256.
+ * Strides are in bytes.  Output `out_dtype` (G9_BF16, the reference default,
+ * or G9_F16).
+ * Replaces kernels/gemm/intra_wave/a4w4/v1_sliceMN/matmul_kernel.py:696-742 (4-wave)
+ * and kernels/gemm/inter_wave/a4w4/v2_mfma32x32x64/matmul_kernel.py:614-668 (8-wave).
+ */
+int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * Bytes of stream-K workspace a call with these arguments needs (0 for the
+ * data-parallel schedule).  `dtype` is the operand type.
+ * No counterpart in the reference (it has no stream-K schedule).
+ */
+size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves);
+
+/*
+ * Zeroes the flag and error words of a stream-K workspace on `stream`.  Call
+ * once after allocating it.  No counterpart in the reference.
+ */
+int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Copies the workspace error word to *error (1 = a stream-K flag wait timed out
+ * and the output is invalid) after synchronising `stream`.  No counterpart in
+ * the reference.
+ */
+int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stream, int* error);
+
+/*
+ * Name of the kernel a call with this (dtype, out_dtype, schedule, waves)
+ * launches, for profiler kernel filters (cf. KERNEL_NAME in
+ * kernels/gemm/inter_wave/a8w8/matmul_kernel.py:52), or NULL.
+ */
+const char* g9_kernel_name(int dtype, int out_dtype, int schedule, int waves);
+
+/* Human-readable text of a status code. */
+const char* g9_status_string(int status);
+
+/* Number of persistent workgroups the stream-K schedule launches on the current device. */
+int g9_streamk_workgroups(void);
+
+/* Library ABI version (major * 100 + minor). */
+int g9_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GFX950_GEMM_H */

@@ -1,0 +1,105 @@
+"""CPU checks of the C ABI: the built library loads, exports exactly the
+entry points include/gfx950_gemm.h declares, and rejects bad arguments with
+the documented status codes before touching the GPU (no launches here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from gfx950_gluon_tutorials_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "gfx950_gemm.h")
+FAKE = 0x10000  # 16-byte aligned non-null address; never dereferenced on these paths
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(g9_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), "binding table out of sync with the header"
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in gfx950_gemm.h but not exported"
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.g9_version() >= 100
+    for code in range(7):
+        assert _lib.status_text(code)
+    assert _lib.status_text(0) == "ok"
+
+
+def test_kernel_names_are_stable_and_unique():
+    names = set()
+    for dt, out in [(_lib.G9_F16, _lib.G9_F16), (_lib.G9_BF16, _lib.G9_BF16), (_lib.G9_BF8, _lib.G9_F16),
+                    (_lib.G9_BF8, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_F16)]:
+        for sched in (_lib.G9_SCHED_DP, _lib.G9_SCHED_SK):
+            n = _lib.kernel_name(dt, out, sched, 4)
+            assert n and n.startswith("g9_a") and n not in names
+            names.add(n)
+    assert _lib.kernel_name(_lib.G9_F16, _lib.G9_BF16, 0, 4) is None
+
+
+def test_workspace_size():
+    lib = _lib.load()
+    assert lib.g9_workspace_size(_lib.G9_F16, 4096, 4096, 8192, _lib.G9_SCHED_DP, 4) == 0
+    sk = lib.g9_workspace_size(_lib.G9_F16, 3840, 3840, 16384, _lib.G9_SCHED_SK, 4)
+    assert sk >= 225 * 256 * 256 * 4 + 225 * 4
+
+
+def _a16w16(M=512, N=512, K=1024, sam=None, sak=1, sbk=1, sbn=None, scm=None, scn=1, dtype=0, sched=0,
+            waves=4, ws=None, ws_bytes=0):
+    lib = _lib.load()
+    return lib.g9_gemm_a16w16(FAKE, FAKE, FAKE, M, N, K, K if sam is None else sam, sak, sbk,
+                              K if sbn is None else sbn, N if scm is None else scm, scn, dtype, sched, waves,
+                              ws, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=0), _lib.G9_ERR_SHAPE),
+    (dict(N=-5), _lib.G9_ERR_SHAPE),
+    (dict(K=100), _lib.G9_ERR_SHAPE),
+    (dict(K=0), _lib.G9_ERR_SHAPE),
+    (dict(sak=2), _lib.G9_ERR_LAYOUT),
+    (dict(sbk=1024, sbn=1), _lib.G9_ERR_LAYOUT),
+    (dict(scn=2), _lib.G9_ERR_LAYOUT),
+    (dict(sam=1000), _lib.G9_ERR_LAYOUT),
+    (dict(dtype=_lib.G9_BF8), _lib.G9_ERR_DTYPE),
+    (dict(dtype=9), _lib.G9_ERR_DTYPE),
+    (dict(waves=3), _lib.G9_ERR_SCHEDULE),
+    (dict(sched=7), _lib.G9_ERR_SCHEDULE),
+    (dict(sched=_lib.G9_SCHED_SK), _lib.G9_ERR_WORKSPACE),
+    (dict(sched=_lib.G9_SCHED_SK, ws=FAKE, ws_bytes=1024), _lib.G9_ERR_WORKSPACE),
+])
+def test_a16w16_argument_validation(kw, code):
+    assert _a16w16(**kw) == code
+
+
+def test_a8w8_and_a4w4_argument_validation():
+    lib = _lib.load()
+    # a8w8: K must be a multiple of 128; output dtype fp16/bf16 only.
+    assert lib.g9_gemm_a8w8(FAKE, FAKE, FAKE, 256, 256, 192, 192, 1, 1, 192, 256, 1, None, None,
+                            _lib.G9_F16, 0, 4, None, 0, None) == _lib.G9_ERR_SHAPE
+    assert lib.g9_gemm_a8w8(FAKE, FAKE, FAKE, 256, 256, 256, 256, 1, 1, 256, 256, 1, None, None,
+                            _lib.G9_BF8, 0, 4, None, 0, None) == _lib.G9_ERR_DTYPE
+    # a4w4: scales must be row-major-ish and wide enough.
+    assert lib.g9_gemm_a4w4(FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 512, 256, 1, 256, 1, 256, 1,
+                            1, 256, 16, 1, _lib.G9_BF16, 0, 4, None, 0, None) == _lib.G9_ERR_LAYOUT
+    assert lib.g9_gemm_a4w4(FAKE, FAKE, FAKE, None, FAKE, 256, 256, 512, 256, 1, 256, 1, 256, 1,
+                            16, 1, 16, 1, _lib.G9_BF16, 0, 4, None, 0, None) == _lib.G9_ERR_LAYOUT
+    assert lib.g9_gemm_a4w4(FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 384, 192, 1, 192, 1, 256, 1,
+                            12, 1, 12, 1, _lib.G9_BF16, 0, 4, None, 0, None) == _lib.G9_ERR_SHAPE
+
+
+def test_status_maps_to_python_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.G9_ERR_SHAPE, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.G9_ERR_HIP, "x")
+    _lib.check(_lib.G9_OK, "x")
