@@ -47,7 +47,25 @@ def parse_args():
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
+    p.add_argument("--summarize", default="",
+                   help="print a per-kernel summary of the rocprofv3 SQLite output under this directory and exit")
+    p.add_argument("--copy-mb", type=int, default=0,
+                   help="also launch a plain device copy of this many MiB 10 times (counter calibration)")
     return p.parse_args()
+
+
+def copy_calibration(mb: int, dev) -> None:
+    """A plain copy kernel of known size: its FETCH_SIZE / WRITE_SIZE readings
+    give the scale between those counters and bytes moved."""
+    import torch
+
+    n = mb * 2**20 // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"# copy calibration: 10 x {mb} MiB device copies", flush=True)
 
 
 def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
@@ -154,6 +172,47 @@ def cpu_baseline(dtype: str, M: int, N: int, K: int, seed: int):
     }
 
 
+def summarize_rocpd(path: str) -> None:
+    """Per-kernel summary of rocprofv3 output (its SQLite ``*_results.db``):
+    dispatch counts and durations from the kernel trace, and per-dispatch
+    medians of every collected counter."""
+    import glob
+    import sqlite3
+    import statistics as st
+
+    dbs = sorted(glob.glob(os.path.join(path, "**", "*.db"), recursive=True))
+    if not dbs:
+        print(f"no rocprofv3 databases under {path}")
+        return
+    for db in dbs:
+        con = sqlite3.connect(db)
+        views = {r[0] for r in con.execute("select name from sqlite_master where type='view'")}
+        print(f"== {os.path.relpath(db, path)}")
+        if "kernels" in views:
+            rows = con.execute("select name, grid_x, duration from kernels order by start").fetchall()
+            groups = {}
+            for name, grid, dur in rows:
+                groups.setdefault((name, grid), []).append(dur / 1e3)
+            if groups:
+                print(f"{'kernel':48s} {'grid':>8s} {'calls':>6s} {'mean_us':>9s} {'median_us':>9s} "
+                      f"{'min_us':>8s} {'max_us':>8s} {'last100_mean_us':>15s}")
+            for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+                print(f"{name[:48]:48s} {grid:8d} {len(d):6d} {st.mean(d):9.2f} {st.median(d):9.2f} "
+                      f"{min(d):8.2f} {max(d):8.2f} {st.mean(d[-100:]):15.2f}")
+        if "counters_collection" in views:
+            rows = con.execute("select kernel_name, grid_size, counter_name, value, duration "
+                               "from counters_collection").fetchall()
+            groups = {}
+            for name, grid, cn, val, dur in rows:
+                g = groups.setdefault((name, grid), {"dur": []})
+                g.setdefault(cn, []).append(val)
+                g["dur"].append(dur / 1e3)
+            for (name, grid), g in sorted(groups.items(), key=lambda kv: -sum(kv[1]["dur"])):
+                n = len(g["dur"]) // max(1, len(g) - 1)
+                vals = "  ".join(f"{cn}={st.median(v):.6g}" for cn, v in sorted(g.items()) if cn != "dur")
+                print(f"{name[:48]:48s} grid={grid} dispatches={n} median_us={st.median(g['dur']):.2f}  {vals}")
+
+
 def load_traffic(key: str):
     try:
         with open(TRAFFIC_FILE) as f:
@@ -164,6 +223,9 @@ def load_traffic(key: str):
 
 def main():
     args = parse_args()
+    if args.summarize:
+        summarize_rocpd(args.summarize)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
@@ -200,6 +262,8 @@ def main():
             print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f} TFLOPS", flush=True)
             del launch
             torch.cuda.empty_cache()
+    if args.copy_mb:
+        copy_calibration(args.copy_mb, dev)
     head = "fp16" if "fp16" in results else dtypes[0]
     r = results[head]
     line = {

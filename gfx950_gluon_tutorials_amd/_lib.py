@@ -13,7 +13,9 @@ import threading
 
 from . import build as _build
 
-LIB_PATH = _build.LIB_PATH
+# G9_LIBRARY overrides the path (e.g. to compare two builds); default: the
+# library built in this package directory.
+LIB_PATH = os.environ.get("G9_LIBRARY") or _build.LIB_PATH
 
 # Status codes (gfx950_gemm.h).
 G9_OK = 0

@@ -79,7 +79,8 @@ static_assert(kTile * kStageRow <= kLdsBytes4w, "staging must fit");
 // (FP4) the lane's 8 raw scale bytes of the stage.
 struct Frag {
   u32x4 c[2];
-  u32x2 sc;
+  u32x2 sc;  // FP4: the lane's 8 raw E8M0 bytes of the stage (groups 0..7)
+  u32 sp;    // FP4: byte 0 = scale of group g (step 0), byte 1 = group 4+g (step 1)
 };
 
 template <Op OP>
@@ -88,8 +89,14 @@ struct OpInfo {
   static constexpr int kSub = OP == Op::BF8 ? 1 : 2;  // MFMAs per fragment pair per stage
   static constexpr int kDmaPerRegion = kScaled ? 5 : 4;
   static constexpr int kMfmaPerRegion = 16 * kSub;
-  // The two 16-byte chunks (of the row's eight) lane group g reads per stage.
-  static G9_DEV int chunk(int e, int g) { return OP == Op::BF8 ? 2 * g + e : 4 * e + g; }
+  // The two 16-byte chunks (of the row's eight) lane group g reads per stage:
+  // chunks g and 4+g.  For FP16/BF16 and FP4 they feed MFMA step e; BF8 feeds
+  // both to one 16x16x128 MFMA, so its lane group g holds K bytes 16g..16g+15
+  // and 64+16g..64+16g+15 instead of a contiguous 32 -- the same K
+  // permutation for A and B, so the dot product is unchanged, and the LDS read
+  // pattern is the FP16 one, which measures free of bank conflicts (the
+  // contiguous 2g, 2g+1 assignment measured 2-way conflicts).
+  static G9_DEV int chunk(int e, int g) { return 4 * e + g; }
 };
 
 // LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
@@ -104,9 +111,9 @@ constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; 
 // hazard recognizer does not see through inline assembly, so the callers
 // insert the MFMA-to-VALU wait states themselves (see mfma_drain) and never
 // feed an MFMA from a VALU result written within a few cycles.
-// `sc` holds the lane's two E8M0 scales (FP4 only).
+// FP4 takes the lane's two E8M0 scales from the fragments' `sp`.
 template <Op OP, int H>
-G9_DEV void mma(f32x4& acc, const Frag& bx, const Frag& ay, u32 scx, u32 scy) {
+G9_DEV void mma(f32x4& acc, const Frag& bx, const Frag& ay) {
   if constexpr (OP == Op::F16) {
     asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[H]), "v"(ay.c[H]));
   } else if constexpr (OP == Op::BF16) {
@@ -123,11 +130,11 @@ G9_DEV void mma(f32x4& acc, const Frag& bx, const Frag& ay, u32 scx, u32 scy) {
     if constexpr (H == 0)
       asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"
           : "+a"(acc)
-          : "v"(bx.c[0]), "v"(ay.c[0]), "v"(scx), "v"(scy));
+          : "v"(bx.c[0]), "v"(ay.c[0]), "v"(bx.sp), "v"(ay.sp));
     else
       asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"
           : "+a"(acc)
-          : "v"(bx.c[1]), "v"(ay.c[1]), "v"(scx), "v"(scy));
+          : "v"(bx.c[1]), "v"(ay.c[1]), "v"(bx.sp), "v"(ay.sp));
   }
 }
 
@@ -141,24 +148,36 @@ G9_DEV void mfma_drain() {
 }
 
 // Where, inside a region of NM MFMAs, the other instructions are issued (they
-// go right after MFMA number k).  The eight 16-byte LDS reads come first so the
-// region-closing lgkmcnt(0) finds them complete; the DMAs are spread evenly so
-// the four waves of a CU keep the texture-address pipe at its issue rate.
+// go right after MFMA number k).  The first kPre MFMAs are issued before the
+// region's s_barrier (their operands are already in registers), so the MFMA
+// pipe stays busy while the barrier resolves; LDS reads and DMAs follow the
+// barrier.  The eight 16-byte LDS reads come first so the region-closing
+// lgkmcnt(0) finds them complete; the DMAs are spread evenly.  FP4 gathers the
+// scale bytes of the set it just read at slot kPermSlot, late enough that the
+// reads are done and early enough that the VALU results are long written when
+// the next region's MFMAs read them.
 template <Op OP>
 struct Slots {
   static constexpr int NM = OpInfo<OP>::kMfmaPerRegion;
+  static constexpr int kPre = OP == Op::BF8 ? 1 : 2;
+  static constexpr int kPermSlot = NM - 8;
   static constexpr int read16(int k) {  // 16-byte read number issued after MFMA k, or -1
-    if constexpr (OP == Op::BF8) return k < 8 ? k : -1;
-    else return (k % 2 == 0 && k < 16) ? k / 2 : -1;
+    const int q = k - kPre;
+    if (q < 0) return -1;
+    if constexpr (OP == Op::BF8) return q < 8 ? q : -1;
+    else return (q % 2 == 0 && q < 16) ? q / 2 : -1;
   }
   static constexpr int read8(int k) {  // FP4 scale-row read number, or -1
-    return (OP == Op::FP4 && k % 4 == 1 && k < 16) ? k / 4 : -1;
+    const int q = k - kPre;
+    return (OP == Op::FP4 && q >= 0 && q % 4 == 1 && q < 16) ? q / 4 : -1;
   }
   static constexpr int dma16(int k) {  // 16-byte DMA number, or -1
-    if constexpr (OP == Op::BF8) return k % 4 == 1 ? k / 4 : -1;
-    else return k % 8 == 1 ? k / 8 : -1;
+    const int q = k - kPre;
+    if (q < 0) return -1;
+    if constexpr (OP == Op::BF8) return q % 4 == 1 ? q / 4 : -1;
+    else return q % 8 == 1 ? q / 8 : -1;
   }
-  static constexpr bool dma4(int k) { return OP == Op::FP4 && k == 5; }
+  static constexpr bool dma4(int k) { return OP == Op::FP4 && k - kPre == 5; }
 };
 
 // Keeps a value in a register the compiler cannot see through, so constant
@@ -283,60 +302,55 @@ struct Pipe {
   }
 };
 
-// Region prologue: all but the last six DMA groups landed and the wave's own
-// LDS reads complete, then the workgroup barrier.  The leading scheduling
-// fence keeps the wait at the region boundary.
-template <Op OP>
-G9_DEV void region_sync() {
-  __builtin_amdgcn_sched_barrier(0);
-  waitcnt<6 * OpInfo<OP>::kDmaPerRegion, 0>();
-  barrier();
-}
-
 // Slot K of a region: MFMA number K (step-major: step, A fragment, B
-// fragment), then whatever the slot table puts after it, then a fence that
-// lets only scalar/vector ALU work move across.
+// fragment), then whatever the slot table puts after it, then a hard
+// scheduling fence (the MFMAs are inline assembly, which the scheduler's
+// instruction-class masks do not cover, so only a full fence pins the order).
 template <Op OP, int RX, int RSLOT, int DX, int DSLOT, int K>
 G9_DEV void region_slot(const Pipe<OP>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, f32x4 (&acc)[4][4],
-                        const Frag (&bx)[4], const Frag (&ay)[4], const u32 (&scx)[4], const u32 (&scy)[4],
-                        Frag (&nxt)[4]) {
+                        const Frag (&bx)[4], const Frag (&ay)[4], Frag (&nxt)[4]) {
   using S = Slots<OP>;
   constexpr int h = K / 16, i = (K / 4) % 4, j = K % 4;
-  mma<OP, h>(acc[i][j], bx[j], ay[i], scx[j], scy[i]);
+  mma<OP, h>(acc[i][j], bx[j], ay[i]);
   if constexpr (S::read16(K) >= 0) P.template read_chunk<RX, RSLOT, S::read16(K)>(nxt);
   if constexpr (S::read8(K) >= 0) P.template read_scales<RX, RSLOT, S::read8(K)>(nxt);
   if constexpr (S::dma16(K) >= 0) P.template dma_rows<DX, DSLOT, S::dma16(K)>(r, soff);
   if constexpr (S::dma4(K)) P.template dma_scales<DX, DSLOT>(rs, soff_sc);
+  if constexpr (OpInfo<OP>::kScaled && K == S::kPermSlot) {
+    waitcnt<63, 0>();
+#pragma unroll
+    for (int f = 0; f < 4; ++f) nxt[f].sp = __builtin_amdgcn_perm(nxt[f].sc.y, nxt[f].sc.x, P.sel);
+  }
   __builtin_amdgcn_sched_barrier(0);
 }
 
 // One quadrant region: MFMAs of (bx, ay) into acc, LDS reads of sub-buffer
 // RX/RSLOT into nxt, DMA of stage `ds` into sub-buffer DX/DSLOT.
+//   s_waitcnt vmcnt(6 groups) lgkmcnt(0)   -- DMA of the set read now landed,
+//                                             the previous region's reads done
+//   kPre MFMAs
+//   s_barrier                              -- every wave's DMA landed and every
+//                                             wave done reading the sub-buffer
+//                                             refilled now
+//   remaining MFMAs with the reads and DMAs interleaved
 template <Op OP, int RX, int RSLOT, int DX, int DSLOT>
 G9_DEV void region(const Pipe<OP>& P, int ds, f32x4 (&acc)[4][4], const Frag (&bx)[4], const Frag (&ay)[4],
                    Frag (&nxt)[4]) {
-  region_sync<OP>();
+  using S = Slots<OP>;
+  __builtin_amdgcn_sched_barrier(0);
+  waitcnt<6 * OpInfo<OP>::kDmaPerRegion, 0>();
   const bool live = ds < P.s_end;
   const rsrc_t r = P.src(DX, live);
   rsrc_t rs = r;
   if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
   const u32 soff = (u32)ds * kRowBytes, soff_sc = (u32)ds * 8;
-  // FP4: gather each fragment's two scale bytes (VALU) before the first MFMA,
-  // with wait states between the last write and the MFMA reads.
-  u32 scx[4] = {0, 0, 0, 0}, scy[4] = {0, 0, 0, 0};
-  if constexpr (OpInfo<OP>::kScaled) {
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      scx[f] = __builtin_amdgcn_perm(bx[f].sc.y, bx[f].sc.x, P.sel);
-      scy[f] = __builtin_amdgcn_perm(ay[f].sc.y, ay[f].sc.x, P.sel);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_nop 4" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  }
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, scx, scy, nxt), ...);
-  }(std::make_integer_sequence<int, Slots<OP>::NM>{});
+    (region_slot<OP, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+  }(std::make_integer_sequence<int, S::kPre>{});
+  barrier();
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    (region_slot<OP, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+  }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
 // Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
@@ -386,6 +400,13 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   P.template load<0, 0>(at);
   P.template load<2, 0>(x);
   waitcnt<6 * I::kDmaPerRegion, 0>();
+  if constexpr (I::kScaled) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      at[f].sp = __builtin_amdgcn_perm(at[f].sc.y, at[f].sc.x, P.sel);
+      x[f].sp = __builtin_amdgcn_perm(x[f].sc.y, x[f].sc.x, P.sel);
+    }
+  }
   barrier();
   P.template issue<0, 0>(s0 + 2);
   // The accumulators were just written by VALU (zeroing or a partial tile):
