@@ -34,6 +34,9 @@ PEAK = {"fp16": 2500.0, "bf16": 2500.0, "bf8": 5000.0, "mxfp4": 10100.0}
 # kernels/gemm/intra_wave/a16w16/v9_beyond_hotloop/README.md:180,
 # kernels/gemm/inter_wave/a8w8/README.md:61, kernels/gemm/inter_wave/a4w4/v0_sliceMN/README.md:60).
 REFERENCE_TFLOPS = {"fp16": 1608.0, "bf8": 3215.0, "mxfp4": 4986.0}
+# 8-wave: kernels/gemm/inter_wave/a16w16/README.md:120, kernels/gemm/inter_wave/a8w8/README.md:61,
+# kernels/gemm/inter_wave/a4w4/README.md:17.
+REFERENCE_TFLOPS_8W = {"fp16": 1478.0, "bf8": 2949.0, "mxfp4": 4479.0}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -44,8 +47,11 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--dtypes", default="fp16,bf8,mxfp4", help="comma list of fp16,bf16,bf8,mxfp4")
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
+    p.add_argument("--waves", default="4,8", help="wave schedules to time: 4 (1 wave/SIMD), 8 (2 waves/SIMD)")
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
+    p.add_argument("--serialized", type=int, default=1,
+                   help="also time the reference's protocol: serialized dispatches, mean of the last 100 of 1000")
     p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
     p.add_argument("--summarize", default="",
                    help="print a per-kernel summary of the rocprofv3 SQLite output under this directory and exit")
@@ -68,14 +74,19 @@ def copy_calibration(mb: int, dev) -> None:
     print(f"# copy calibration: 10 x {mb} MiB device copies", flush=True)
 
 
-def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
-    """Returns (launch(i) -> None, bytes per set)."""
+def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int, waves: int = 4):
+    """Returns launch(i, schedule) running the drop-in wrapper of `waves` on operand set i."""
     import torch
 
     from gfx950_gluon_tutorials_amd import quant
-    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a4w4 import matmul as m4
-    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a8w8 import matmul as m8
-    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as m16
+    if waves == 4:
+        from gfx950_gluon_tutorials_amd.gemm.intra_wave.a4w4 import matmul as m4
+        from gfx950_gluon_tutorials_amd.gemm.intra_wave.a8w8 import matmul as m8
+        from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as m16
+    else:
+        from gfx950_gluon_tutorials_amd.gemm.inter_wave.a4w4 import matmul as m4
+        from gfx950_gluon_tutorials_amd.gemm.inter_wave.a8w8 import matmul as m8
+        from gfx950_gluon_tutorials_amd.gemm.inter_wave.a16w16 import matmul as m16
 
     gen = torch.Generator().manual_seed(seed)
     sets = []
@@ -131,6 +142,28 @@ def time_case(launch, steps, warmup, schedule="dp"):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms per launch
+
+
+def time_serialized(launch, n=1000, last=100):
+    """The reference's timing protocol (kernels/gemm/README.md:89-94): every
+    dispatch completes before the next is issued (as with
+    AMD_SERIALIZE_KERNEL=3), each one's duration is taken from events around
+    it, and the mean of the last `last` of `n` is reported (ms)."""
+    import torch
+
+    start = [torch.cuda.Event(enable_timing=True) for _ in range(last)]
+    stop = [torch.cuda.Event(enable_timing=True) for _ in range(last)]
+    launch(0)
+    torch.cuda.synchronize()
+    for i in range(n):
+        j = i - (n - last)
+        if j >= 0:
+            start[j].record()
+        launch(i)
+        if j >= 0:
+            stop[j].record()
+        torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / last
 
 
 def cpu_baseline(dtype: str, M: int, N: int, K: int, seed: int):
@@ -240,16 +273,27 @@ def main():
         dtypes = [args.only]
     seeds = {"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3}
     results = {}
+    waves = [int(w) for w in args.waves.split(",") if w]
     for dt in dtypes:
-        nsets = max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, M, N, K)))
-        launch = make_case(dt, M, N, K, seeds[dt], dev, nsets)
-        ms = time_case(launch, args.steps, args.warmup)
-        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        results[dt] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
-                       "reference_tflops": REFERENCE_TFLOPS.get(dt), "rotating_sets": nsets}
-        print(f"# {dt}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak", flush=True)
-        del launch
-        torch.cuda.empty_cache()
+        for w in waves:
+            nsets = max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, M, N, K)))
+            launch = make_case(dt, M, N, K, seeds[dt], dev, nsets, w)
+            ms = time_case(launch, args.steps, args.warmup)
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            key = dt if w == 4 else f"{dt}_8w"
+            results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
+                            "reference_tflops": REFERENCE_TFLOPS.get(dt) if w == 4 else REFERENCE_TFLOPS_8W.get(dt),
+                            "rotating_sets": nsets, "waves": w}
+            msg = f"# {key}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak"
+            if args.serialized:
+                ms_s = time_serialized(launch)
+                tf_s = 2.0 * M * N * K / (ms_s * 1e-3) / 1e12
+                results[key]["serialized_tflops"] = round(tf_s, 2)
+                results[key]["serialized_ms"] = round(ms_s, 5)
+                msg += f"  | serialized (reference protocol) {ms_s * 1e3:.1f} us {tf_s:.1f} TFLOPS"
+            print(msg, flush=True)
+            del launch
+            torch.cuda.empty_cache()
     sk = {}
     if args.streamk and not args.only:
         for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192)]:
@@ -264,7 +308,7 @@ def main():
             torch.cuda.empty_cache()
     if args.copy_mb:
         copy_calibration(args.copy_mb, dev)
-    head = "fp16" if "fp16" in results else dtypes[0]
+    head = "fp16" if "fp16" in results else next(iter(results))
     r = results[head]
     line = {
         "metric": "TFLOPS & % of MFMA peak, 4096x4096x8192 fp16/bf8/mxfp4, 1xMI355X",
@@ -277,18 +321,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(r["tflops"] / REFERENCE_TFLOPS[head], 4) if head in REFERENCE_TFLOPS else None,
-        "dtype": head,
+        "dtype": head.split("_")[0],
         "data": "synthetic",
         "config": {"workload": f"{head} NT GEMM C=A.B^T, M=N=4096, K=8192, 256x256 tiles, data-parallel, 4-wave; "
                                f"operands rotate over {r['rotating_sets']} resident sets",
                    "M": M, "N": N, "K": K},
-        "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK[head], "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK[head.split("_")[0]], "unit": "TFLOP/s",
                      "frac": r["frac_of_peak"], "traffic": load_traffic(f"{head}_{M}x{N}x{K}")},
         "per_dtype": results,
         "streamk": sk,
     }
     if args.cpu_baseline and not args.only:
-        line["cpu_baseline"] = cpu_baseline(head, M, N, K, seeds[head])
+        line["cpu_baseline"] = cpu_baseline(head.split("_")[0], M, N, K, seeds[head.split("_")[0]])
     print(json.dumps(line), flush=True)
 
 

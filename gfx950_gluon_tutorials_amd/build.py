@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libg9gemm.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["g9_capi.hip"]
-HEADERS = ["g9_common.hpp", "g9_gemm_4w.hpp"]
+HEADERS = ["g9_common.hpp", "g9_gemm.hpp"]
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_*_f32, whose results
 # have been unreliable on the target machines.

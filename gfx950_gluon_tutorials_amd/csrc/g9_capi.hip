@@ -5,7 +5,7 @@
 #include <mutex>
 
 #include "../../include/gfx950_gemm.h"
-#include "g9_gemm_4w.hpp"
+#include "g9_gemm.hpp"
 
 using namespace g9;
 
@@ -13,18 +13,21 @@ using namespace g9;
 // Named kernels: one symbol per (operand type, output type, schedule, waves) so
 // profilers can filter on a stable substring.
 // ---------------------------------------------------------------------------
-#define G9_ATTRS __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+#define G9_ATTRS(G) \
+  __launch_bounds__(G::kThreads) __attribute__((amdgpu_waves_per_eu(G::kWavesPerSimd, G::kWavesPerSimd)))
 
-#define G9_DEFINE_4W(NAME, OP, OUT)                                                         \
-  extern "C" __global__ G9_ATTRS void NAME##_dp_4w(GemmParams p) { gemm_dp_4w<OP, OUT>(p); } \
-  extern "C" __global__ G9_ATTRS void NAME##_sk_4w(GemmParams p) { gemm_sk_4w<OP, OUT>(p); }
+#define G9_DEFINE(NAME, OP, OUT)                                                                      \
+  extern "C" __global__ G9_ATTRS(Geo4) void NAME##_dp_4w(GemmParams p) { gemm_dp<OP, OUT, Geo4>(p); } \
+  extern "C" __global__ G9_ATTRS(Geo4) void NAME##_sk_4w(GemmParams p) { gemm_sk<OP, OUT, Geo4>(p); } \
+  extern "C" __global__ G9_ATTRS(Geo8) void NAME##_dp_8w(GemmParams p) { gemm_dp<OP, OUT, Geo8>(p); } \
+  extern "C" __global__ G9_ATTRS(Geo8) void NAME##_sk_8w(GemmParams p) { gemm_sk<OP, OUT, Geo8>(p); }
 
-G9_DEFINE_4W(g9_a16w16_f16, Op::F16, OUT_F16)
-G9_DEFINE_4W(g9_a16w16_bf16, Op::BF16, OUT_BF16)
-G9_DEFINE_4W(g9_a8w8_f16out, Op::BF8, OUT_F16)
-G9_DEFINE_4W(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
-G9_DEFINE_4W(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
-G9_DEFINE_4W(g9_a4w4_f16out, Op::FP4, OUT_F16)
+G9_DEFINE(g9_a16w16_f16, Op::F16, OUT_F16)
+G9_DEFINE(g9_a16w16_bf16, Op::BF16, OUT_BF16)
+G9_DEFINE(g9_a8w8_f16out, Op::BF8, OUT_F16)
+G9_DEFINE(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
+G9_DEFINE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
+G9_DEFINE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
 typedef void (*KernelFn)(GemmParams);
 
@@ -36,10 +39,11 @@ struct KernelEntry {
   const char* name;
 };
 
-#define G9_ENTRY(DT, OUT, NAME)                                             \
-  {DT, OUT, G9_SCHED_DP, 4, NAME##_dp_4w, #NAME "_dp_4w"},                  \
-  {                                                                         \
-    DT, OUT, G9_SCHED_SK, 4, NAME##_sk_4w, #NAME "_sk_4w"                   \
+#define G9_ENTRY(DT, OUT, NAME)                                                                   \
+  {DT, OUT, G9_SCHED_DP, 4, NAME##_dp_4w, #NAME "_dp_4w"}, {DT, OUT, G9_SCHED_SK, 4, NAME##_sk_4w, #NAME "_sk_4w"}, \
+      {DT, OUT, G9_SCHED_DP, 8, NAME##_dp_8w, #NAME "_dp_8w"},                                               \
+  {                                                                                               \
+    DT, OUT, G9_SCHED_SK, 8, NAME##_sk_8w, #NAME "_sk_8w"                                       \
   }
 
 const KernelEntry kKernels[] = {
@@ -97,7 +101,7 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // generic checks done here.
 int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
            void* stream) {
-  if (waves != 4) return G9_ERR_SCHEDULE;
+  if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
   if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK) return G9_ERR_SCHEDULE;
   const KernelEntry* k = find_kernel(dtype, out, schedule, waves);
   if (!k) return G9_ERR_DTYPE;
@@ -124,7 +128,7 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     grid = (int)(units < cus ? units : cus);
     p.sk_ctas = grid;
   }
-  hipLaunchKernelGGL(k->fn, dim3(grid), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL(k->fn, dim3(grid), dim3(64 * waves), 0, s, p);
   return hipGetLastError() == hipSuccess ? G9_OK : G9_ERR_HIP;
 }
 

@@ -1,9 +1,13 @@
-// 4-wave (one wave per SIMD) NT GEMM for gfx950: C[M,N] = A[M,K] . B[N,K]^T.
+// NT GEMM kernels for gfx950: C[M,N] = A[M,K] . B[N,K]^T.
 //
-// One workgroup = 256 threads = 4 waves computes a 256x256 output tile.  The
-// tile is four 128x128 quadrants; wave (wm, wn) owns the 64x64 piece of every
-// quadrant at (wm*64, wn*64), i.e. 2x2 quadrants x 4x4 MFMA 16x16 fragments x
-// 4 fp32 = 256 accumulator registers per lane (they live in AGPRs).
+// One workgroup computes a 256x256 output tile, split into four 128x128
+// quadrants.  Two wave geometries share all the code below:
+//   * 4-wave (G = Geo4, 1 wave per SIMD): waves 2x2, each owns the 64x64 piece
+//     of every quadrant -> 2x2x4x4 MFMA 16x16 fragments x 4 fp32 = 256
+//     accumulators per lane (AGPRs).
+//   * 8-wave (G = Geo8, 2 waves per SIMD): waves 2x4, each owns a 64x32 piece
+//     of every quadrant -> 128 accumulators per lane.  While one wave of a SIMD
+//     waits (barrier, counters, DMA issue) the other issues its MFMAs.
 //
 // K is walked in stages of 128 bytes per operand row: 64 fp16/bf16, 128 bf8 or
 // 256 fp4 values.  A stage is split into four LDS sub-buffers of 128 rows x 128
@@ -16,11 +20,11 @@
 // issues its MFMAs on operand fragments already in registers, reads the next
 // region's operand set from LDS into registers, and refills, by LDS-DMA, the
 // sub-buffer whose last reads finished in the previous region.  A region
-// starts with `s_waitcnt vmcnt(6 groups) lgkmcnt(0); s_barrier`: the sub-buffer
-// read during a region was requested seven regions earlier, so the DMA latency
-// budget is 1.5 stages (~3000 MFMA cycles) and one barrier per region suffices.
-// The B operand registers alternate roles between even and odd stages, so the
-// loop body covers two stages.
+// starts with `s_waitcnt vmcnt(6 groups) lgkmcnt(0)`, issues its first MFMAs,
+// then `s_barrier`: the sub-buffer read during a region was requested seven
+// regions earlier, so the DMA latency budget is 1.5 stages and one barrier per
+// region suffices.  The B operand registers alternate roles between even and
+// odd stages, so the loop body covers two stages.
 //
 // LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk slot
 // c ^ ((r >> 1) & 7).  A ds_read_b128 by 16 consecutive lanes (16 rows, one
@@ -67,13 +71,31 @@ struct GemmParams {
 };
 
 constexpr int kTile = 256;
-constexpr int kThreads = 256;
 constexpr int kRowBytes = 128;              // bytes of one operand row per stage
 constexpr int kSubBytes = 128 * kRowBytes;  // one sub-buffer (16 KiB)
 constexpr int kScaleBase = 131072;          // FP4 scale sub-buffers (8 x 1 KiB)
 constexpr int kStageRow = 528;              // epilogue staging row pitch (bytes)
-constexpr int kLdsBytes4w = 139264;         // 128 KiB operands + 8 KiB scales
-static_assert(kTile * kStageRow <= kLdsBytes4w, "staging must fit");
+constexpr int kLdsBytes = 139264;           // 128 KiB operands + 8 KiB scales
+static_assert(kTile * kStageRow <= kLdsBytes, "staging must fit");
+
+// Wave geometry: NW waves as WM x WN; per quadrant a wave owns FM x FN MFMA
+// 16x16 fragments (FM*16 rows of A, FN*16 rows of B).
+template <int NW_, int WM_, int WN_>
+struct Geo {
+  static constexpr int NW = NW_, WM = WM_, WN = WN_;
+  static constexpr int kThreads = 64 * NW;
+  static constexpr int FM = 128 / 16 / WM, FN = 128 / 16 / WN;
+  static constexpr int kDmaRows = 128 / NW;        // rows of each sub-buffer one wave loads
+  static constexpr int kDmaPerSub = kDmaRows / 8;  // 16-byte DMAs per wave per sub-buffer
+  // FP4 scale DMA: one dword per lane, kDmaRows rows of 8 bytes per wave, so
+  // 2*kDmaRows lanes are active (all 64 for 4 waves, 32 for 8 waves; a
+  // sub-dword LDS-DMA still writes each lane at a 4-byte stride, so it cannot
+  // pack the 8-wave share into fewer bytes per lane).
+  static constexpr int kScaleLanes = 2 * kDmaRows;
+  static constexpr int kWavesPerSimd = NW / 4;
+};
+using Geo4 = Geo<4, 2, 2>;
+using Geo8 = Geo<8, 2, 4>;
 
 // Operand fragment of one 16-row slice for one stage: 32 bytes per lane, plus
 // (FP4) the lane's 8 raw scale bytes of the stage.
@@ -87,8 +109,6 @@ template <Op OP>
 struct OpInfo {
   static constexpr bool kScaled = OP == Op::FP4;
   static constexpr int kSub = OP == Op::BF8 ? 1 : 2;  // MFMAs per fragment pair per stage
-  static constexpr int kDmaPerRegion = kScaled ? 5 : 4;
-  static constexpr int kMfmaPerRegion = 16 * kSub;
   // The two 16-byte chunks (of the row's eight) lane group g reads per stage:
   // chunks g and 4+g.  For FP16/BF16 and FP4 they feed MFMA step e; BF8 feeds
   // both to one 16x16x128 MFMA, so its lane group g holds K bytes 16g..16g+15
@@ -99,6 +119,12 @@ struct OpInfo {
   static G9_DEV int chunk(int e, int g) { return 4 * e + g; }
 };
 
+template <Op OP, class G>
+struct Shape {
+  static constexpr int NM = G::FM * G::FN * OpInfo<OP>::kSub;  // MFMAs per wave per region
+  static constexpr int kDmaPerRegion = G::kDmaPerSub + (OpInfo<OP>::kScaled ? 1 : 0);
+};
+
 // LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
 constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s) * kSubBytes; }
 constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; }
@@ -106,8 +132,8 @@ constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; 
 // One MFMA of step H of the stage on a (B fragment, A fragment) pair, written
 // as inline assembly with the accumulator tied in place ("+a").  The compiler
 // selects an untied MFMA form for the builtins and then renames every
-// accumulator chain across the 256 AGPRs, which costs hundreds of AGPR copies
-// per loop iteration; the tied form keeps each chain in its registers.  The
+// accumulator chain across the AGPRs, which costs hundreds of AGPR copies per
+// loop iteration; the tied form keeps each chain in its registers.  The
 // hazard recognizer does not see through inline assembly, so the callers
 // insert the MFMA-to-VALU wait states themselves (see mfma_drain) and never
 // feed an MFMA from a VALU result written within a few cycles.
@@ -151,33 +177,44 @@ G9_DEV void mfma_drain() {
 // go right after MFMA number k).  The first kPre MFMAs are issued before the
 // region's s_barrier (their operands are already in registers), so the MFMA
 // pipe stays busy while the barrier resolves; LDS reads and DMAs follow the
-// barrier.  The eight 16-byte LDS reads come first so the region-closing
-// lgkmcnt(0) finds them complete; the DMAs are spread evenly.  FP4 gathers the
-// scale bytes of the set it just read at slot kPermSlot, late enough that the
-// reads are done and early enough that the VALU results are long written when
-// the next region's MFMAs read them.
-template <Op OP>
+// barrier.  The region's NR 16-byte LDS reads come first, spread over a window
+// of W slots, so the region-closing lgkmcnt(0) finds them complete; the DMAs
+// are spread over the whole region.  FP4 gathers the scale bytes of the set it
+// just read at slot kPermSlot, after its reads and well before the next
+// region's MFMAs read the results.
+template <Op OP, class G, int NF>
 struct Slots {
-  static constexpr int NM = OpInfo<OP>::kMfmaPerRegion;
-  static constexpr int kPre = OP == Op::BF8 ? 1 : 2;
-  static constexpr int kPermSlot = NM - 8;
-  static constexpr int read16(int k) {  // 16-byte read number issued after MFMA k, or -1
+  using SH = Shape<OP, G>;
+  static constexpr int NM = SH::NM;
+  static constexpr int kPre = (OP == Op::BF8 || G::NW == 8) ? 1 : 2;
+  static constexpr int NQ = NM - kPre;  // slots after the barrier
+  static constexpr int NR = 2 * NF;     // 16-byte reads of the set loaded in this region
+  static constexpr int W = NQ < (NR > NQ / 2 ? NR : NQ / 2) ? NQ : (NR > NQ / 2 ? NR : NQ / 2);
+  // reads issued after MFMA k: [first_read(k), first_read(k + 1))
+  static constexpr int first_read(int k) {
     const int q = k - kPre;
-    if (q < 0) return -1;
-    if constexpr (OP == Op::BF8) return q < 8 ? q : -1;
-    else return (q % 2 == 0 && q < 16) ? q / 2 : -1;
+    if (q <= 0) return 0;
+    if (q >= W) return NR;
+    return (q * NR + W - 1) / W;
   }
+  static constexpr int kLastReadSlot = kPre + W - 1;
+  static constexpr int kRead8Step = (W + NF - 1) / NF;
   static constexpr int read8(int k) {  // FP4 scale-row read number, or -1
-    const int q = k - kPre;
-    return (OP == Op::FP4 && q >= 0 && q % 4 == 1 && q < 16) ? q / 4 : -1;
+    const int q = k - kPre - 1;
+    return (OpInfo<OP>::kScaled && q >= 0 && q % kRead8Step == 0 && q / kRead8Step < NF) ? q / kRead8Step : -1;
   }
   static constexpr int dma16(int k) {  // 16-byte DMA number, or -1
     const int q = k - kPre;
-    if (q < 0) return -1;
-    if constexpr (OP == Op::BF8) return q % 4 == 1 ? q / 4 : -1;
-    else return q % 8 == 1 ? q / 8 : -1;
+    constexpr int D = G::kDmaPerSub;
+    constexpr int step = (NQ - 1) / D;
+    return (q >= 1 && (q - 1) % step == 0 && (q - 1) / step < D) ? (q - 1) / step : -1;
   }
-  static constexpr bool dma4(int k) { return OP == Op::FP4 && k - kPre == 5; }
+  static constexpr bool dma_scale(int k) { return OpInfo<OP>::kScaled && k - kPre == 5; }
+  static constexpr int kLastRead8Slot = kPre + 1 + (NF - 1) * kRead8Step;
+  static constexpr int kAfterReads = (kLastReadSlot > kLastRead8Slot ? kLastReadSlot : kLastRead8Slot) + 3;
+  static constexpr int kPermSlot =
+      (kAfterReads > NM - 8 ? kAfterReads : NM - 8) < NM - 1 ? (kAfterReads > NM - 8 ? kAfterReads : NM - 8) : NM - 1;
+  static_assert(!OpInfo<OP>::kScaled || kLastRead8Slot < NM, "scale reads must fit the region");
 };
 
 // Keeps a value in a register the compiler cannot see through, so constant
@@ -189,12 +226,13 @@ G9_DEV u32 opaque(u32 x) {
 
 // Per-workgroup pipeline state: buffer resources, per-lane DMA offsets and LDS
 // read bases.  One instance per output tile (rebuilt per stream-K segment).
-template <Op OP>
+template <Op OP, class G>
 struct Pipe {
   using I = OpInfo<OP>;
+  static constexpr int D = G::kDmaPerSub;
   rsrc_t rA[2], rB[2], rZ;  // operand half-tiles; rZ has no valid bytes (reads 0)
   rsrc_t rSA[2], rSB[2];    // FP4 scale half-tiles
-  u32 vA[4], vB[4];         // DMA offsets of the wave's four 1-KiB runs
+  u32 vA[D], vB[D];         // DMA offsets of the wave's 1-KiB runs
   u32 vSA, vSB;             // FP4 scale DMA offsets
   u32 bA[2], bB[2];         // LDS read bases of the lane's two chunks (A at 0, B at 64 KiB)
   u32 bSA, bSB;             // FP4 LDS read bases of the lane's scale row (at 128 KiB)
@@ -209,7 +247,7 @@ struct Pipe {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / G::WN, wn = wave % G::WN;
     const int g = lane >> 4, r16 = lane & 15;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -224,9 +262,9 @@ struct Pipe {
     }
     rZ = make_rsrc(p.a, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 32 * wave + 8 * j + (lane >> 3);
-      const int ch = (lane & 7) ^ (4 * (j & 1) + (lane >> 4));
+    for (int j = 0; j < D; ++j) {
+      const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
+      const int ch = (lane & 7) ^ ((row >> 1) & 7);
       vA[j] = (u32)row * p.lda + ch * 16;
       vB[j] = (u32)row * p.ldb + ch * 16;
     }
@@ -234,15 +272,16 @@ struct Pipe {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int slot = I::chunk(e, g) ^ sw;
-      bA[e] = opaque(lds0 + (u32)(wm * 64 + r16) * kRowBytes + slot * 16);
-      bB[e] = opaque(lds0 + 65536u + (u32)(wn * 64 + r16) * kRowBytes + slot * 16);
+      bA[e] = opaque(lds0 + (u32)(wm * G::FM * 16 + r16) * kRowBytes + slot * 16);
+      bB[e] = opaque(lds0 + 65536u + (u32)(wn * G::FN * 16 + r16) * kRowBytes + slot * 16);
     }
     if constexpr (I::kScaled) {
-      const int row = 32 * wave + (lane >> 1);
+      // Each wave loads kDmaRows scale rows of 8 bytes, two dwords per row.
+      const int row = G::kDmaRows * wave + (lane >> 1);
       vSA = (u32)row * p.ldsa + (lane & 1) * 4;
       vSB = (u32)row * p.ldsb + (lane & 1) * 4;
-      bSA = opaque(lds0 + kScaleBase + (u32)(wm * 64 + r16) * 8);
-      bSB = opaque(lds0 + kScaleBase + (u32)(wn * 64 + r16) * 8);
+      bSA = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * 16 + r16) * 8);
+      bSB = opaque(lds0 + kScaleBase + (u32)(wn * G::FN * 16 + r16) * 8);
       sel = (u32)g | ((u32)(4 + g) << 8) | 0x0c0c0000u;
     } else {
       sel = 0;
@@ -252,16 +291,22 @@ struct Pipe {
   G9_DEV rsrc_t src(int X, bool live) const { return live ? (X < 2 ? rA[X & 1] : rB[X & 1]) : rZ; }
   G9_DEV rsrc_t src_sc(int X, bool live) const { return live ? (X < 2 ? rSA[X & 1] : rSB[X & 1]) : rZ; }
 
-  // 16-byte DMA number J (rows 8J..8J+7 of the wave's 32) of sub-buffer X.
+  // 16-byte DMA number J (rows 8J..8J+7 of the wave's kDmaRows) of sub-buffer X.
   template <int X, int SLOT, int J>
   G9_DEV void dma_rows(rsrc_t r, u32 soff) const {
-    const u32 dst = lds0 + sub_off(X, SLOT) + (u32)wave * 4096u + J * 1024;
+    const u32 dst = lds0 + sub_off(X, SLOT) + (u32)wave * (G::kDmaRows * kRowBytes) + J * 1024;
     dma16(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
   }
   template <int X, int SLOT>
   G9_DEV void dma_scales(rsrc_t r, u32 soff) const {
-    const u32 dst = lds0 + scale_off(X, SLOT) + (u32)wave * 256u;
-    dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
+    const u32 dst = lds0 + scale_off(X, SLOT) + (u32)wave * (G::kDmaRows * 8);
+    if constexpr (G::kScaleLanes == 64) {
+      dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
+    } else {
+      // Lanes beyond the wave's rows are masked off; the instruction is still
+      // issued by every wave, so vmcnt counts stay uniform.
+      if ((threadIdx.x & 63) < G::kScaleLanes) dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
+    }
   }
 
   // 16-byte LDS read number R (fragment R/2, chunk R%2) of sub-buffer X.
@@ -285,41 +330,54 @@ struct Pipe {
     const bool live = stage < s_end;
     const rsrc_t r = src(X, live);
     const u32 soff = (u32)stage * kRowBytes;
-    dma_rows<X, SLOT, 0>(r, soff);
-    dma_rows<X, SLOT, 1>(r, soff);
-    dma_rows<X, SLOT, 2>(r, soff);
-    dma_rows<X, SLOT, 3>(r, soff);
+    [&]<int... J>(std::integer_sequence<int, J...>) { (dma_rows<X, SLOT, J>(r, soff), ...); }(
+        std::make_integer_sequence<int, D>{});
     if constexpr (I::kScaled) dma_scales<X, SLOT>(src_sc(X, live), (u32)stage * 8);
   }
   template <int X, int SLOT>
   G9_DEV void load(Frag (&f)[4]) const {
+    constexpr int NF = X < 2 ? G::FM : G::FN;
     [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
-        std::make_integer_sequence<int, 8>{});
+        std::make_integer_sequence<int, 2 * NF>{});
     if constexpr (I::kScaled) {
       [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SLOT, F>(f), ...); }(
-          std::make_integer_sequence<int, 4>{});
+          std::make_integer_sequence<int, NF>{});
     }
   }
+  template <int X>
+  G9_DEV void gather_scales(Frag (&f)[4]) const {
+    constexpr int NF = X < 2 ? G::FM : G::FN;
+#pragma unroll
+    for (int i = 0; i < NF; ++i) f[i].sp = __builtin_amdgcn_perm(f[i].sc.y, f[i].sc.x, sel);
+  }
 };
+
+// Per-quadrant accumulators of one wave.
+template <class G>
+using QAcc = f32x4[G::FM][G::FN];
+template <class G>
+using Acc = f32x4[2][2][G::FM][G::FN];
 
 // Slot K of a region: MFMA number K (step-major: step, A fragment, B
 // fragment), then whatever the slot table puts after it, then a hard
 // scheduling fence (the MFMAs are inline assembly, which the scheduler's
 // instruction-class masks do not cover, so only a full fence pins the order).
-template <Op OP, int RX, int RSLOT, int DX, int DSLOT, int K>
-G9_DEV void region_slot(const Pipe<OP>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, f32x4 (&acc)[4][4],
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int K>
+G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, QAcc<G>& acc,
                         const Frag (&bx)[4], const Frag (&ay)[4], Frag (&nxt)[4]) {
-  using S = Slots<OP>;
-  constexpr int h = K / 16, i = (K / 4) % 4, j = K % 4;
+  constexpr int NF = RX < 2 ? G::FM : G::FN;
+  using S = Slots<OP, G, NF>;
+  constexpr int h = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j = K % G::FN;
   mma<OP, h>(acc[i][j], bx[j], ay[i]);
-  if constexpr (S::read16(K) >= 0) P.template read_chunk<RX, RSLOT, S::read16(K)>(nxt);
+  [&]<int... R>(std::integer_sequence<int, R...>) {
+    (P.template read_chunk<RX, RSLOT, S::first_read(K) + R>(nxt), ...);
+  }(std::make_integer_sequence<int, S::first_read(K + 1) - S::first_read(K)>{});
   if constexpr (S::read8(K) >= 0) P.template read_scales<RX, RSLOT, S::read8(K)>(nxt);
   if constexpr (S::dma16(K) >= 0) P.template dma_rows<DX, DSLOT, S::dma16(K)>(r, soff);
-  if constexpr (S::dma4(K)) P.template dma_scales<DX, DSLOT>(rs, soff_sc);
+  if constexpr (S::dma_scale(K)) P.template dma_scales<DX, DSLOT>(rs, soff_sc);
   if constexpr (OpInfo<OP>::kScaled && K == S::kPermSlot) {
     waitcnt<63, 0>();
-#pragma unroll
-    for (int f = 0; f < 4; ++f) nxt[f].sp = __builtin_amdgcn_perm(nxt[f].sc.y, nxt[f].sc.x, P.sel);
+    P.template gather_scales<RX>(nxt);
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -333,55 +391,55 @@ G9_DEV void region_slot(const Pipe<OP>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 so
 //                                             wave done reading the sub-buffer
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
-template <Op OP, int RX, int RSLOT, int DX, int DSLOT>
-G9_DEV void region(const Pipe<OP>& P, int ds, f32x4 (&acc)[4][4], const Frag (&bx)[4], const Frag (&ay)[4],
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT>
+G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const Frag (&bx)[4], const Frag (&ay)[4],
                    Frag (&nxt)[4]) {
-  using S = Slots<OP>;
+  constexpr int NF = RX < 2 ? G::FM : G::FN;
+  using S = Slots<OP, G, NF>;
   __builtin_amdgcn_sched_barrier(0);
-  waitcnt<6 * OpInfo<OP>::kDmaPerRegion, 0>();
+  waitcnt<6 * Shape<OP, G>::kDmaPerRegion, 0>();
   const bool live = ds < P.s_end;
   const rsrc_t r = P.src(DX, live);
   rsrc_t rs = r;
   if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
   const u32 soff = (u32)ds * kRowBytes, soff_sc = (u32)ds * 8;
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::kPre>{});
   barrier();
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
 // Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
 // they are consumed the next stage's B0 fragments go to y as well.
-template <Op OP>
-G9_DEV void stage_even(const Pipe<OP>& P, int s, f32x4 (&acc)[2][2][4][4], Frag (&at)[4], Frag (&ab)[4],
-                       Frag (&x)[4], Frag (&y)[4]) {
-  region<OP, 3, 0, 2, 0>(P, s + 2, acc[0][0], x, at, y);
-  region<OP, 1, 0, 3, 0>(P, s + 2, acc[0][1], y, at, ab);
-  region<OP, 0, 1, 1, 0>(P, s + 2, acc[1][1], y, ab, at);
-  region<OP, 2, 1, 0, 1>(P, s + 3, acc[1][0], x, ab, y);
+template <Op OP, class G>
+G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, Frag (&at)[4], Frag (&ab)[4], Frag (&x)[4],
+                       Frag (&y)[4]) {
+  region<OP, G, 3, 0, 2, 0>(P, s + 2, acc[0][0], x, at, y);
+  region<OP, G, 1, 0, 3, 0>(P, s + 2, acc[0][1], y, at, ab);
+  region<OP, G, 0, 1, 1, 0>(P, s + 2, acc[1][1], y, ab, at);
+  region<OP, G, 2, 1, 0, 1>(P, s + 3, acc[1][0], x, ab, y);
 }
 
 // Odd stage (slot 1): B0 fragments in y; B1 fragments go to x, then the next
 // stage's B0 fragments.
-template <Op OP>
-G9_DEV void stage_odd(const Pipe<OP>& P, int s, f32x4 (&acc)[2][2][4][4], Frag (&at)[4], Frag (&ab)[4],
-                      Frag (&x)[4], Frag (&y)[4]) {
-  region<OP, 3, 1, 2, 1>(P, s + 2, acc[0][0], y, at, x);
-  region<OP, 1, 1, 3, 1>(P, s + 2, acc[0][1], x, at, ab);
-  region<OP, 0, 0, 1, 1>(P, s + 2, acc[1][1], x, ab, at);
-  region<OP, 2, 0, 0, 0>(P, s + 3, acc[1][0], y, ab, x);
+template <Op OP, class G>
+G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, Frag (&at)[4], Frag (&ab)[4], Frag (&x)[4],
+                      Frag (&y)[4]) {
+  region<OP, G, 3, 1, 2, 1>(P, s + 2, acc[0][0], y, at, x);
+  region<OP, G, 1, 1, 3, 1>(P, s + 2, acc[0][1], x, at, ab);
+  region<OP, G, 0, 0, 1, 1>(P, s + 2, acc[1][1], x, ab, at);
+  region<OP, G, 2, 0, 0, 0>(P, s + 3, acc[1][0], y, ab, x);
 }
 
 // Accumulates stages [s0, s1) of tile (tm, tn) into acc.  Leaves every DMA
 // complete and the workgroup synchronised, so LDS is free on return.
-template <Op OP>
-G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1,
-                     f32x4 (&acc)[2][2][4][4]) {
-  using I = OpInfo<OP>;
-  Pipe<OP> P;
+template <Op OP, class G>
+G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, Acc<G>& acc) {
+  constexpr int DQ = Shape<OP, G>::kDmaPerRegion;
+  Pipe<OP, G> P;
   P.init(p, smem, tm, tn, s1);
   // DMA stream order: per stage A0, B0, B1, A1.  Stage s lives in slot (s-s0)&1.
   P.template issue<0, 0>(s0);
@@ -394,18 +452,15 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   P.template issue<1, 1>(s0 + 1);
   // A0(s0) and B0(s0) landed: read them, then (once every wave has) refill
   // A0 slot 0 with stage s0+2.
-  waitcnt<6 * I::kDmaPerRegion, 0>();
+  waitcnt<6 * DQ, 0>();
   barrier();
   Frag at[4], ab[4], x[4], y[4];
   P.template load<0, 0>(at);
   P.template load<2, 0>(x);
-  waitcnt<6 * I::kDmaPerRegion, 0>();
-  if constexpr (I::kScaled) {
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      at[f].sp = __builtin_amdgcn_perm(at[f].sc.y, at[f].sc.x, P.sel);
-      x[f].sp = __builtin_amdgcn_perm(x[f].sc.y, x[f].sc.x, P.sel);
-    }
+  waitcnt<6 * DQ, 0>();
+  if constexpr (OpInfo<OP>::kScaled) {
+    P.template gather_scales<0>(at);
+    P.template gather_scales<2>(x);
   }
   barrier();
   P.template issue<0, 0>(s0 + 2);
@@ -426,46 +481,47 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   barrier();
 }
 
-G9_DEV void zero_acc(f32x4 (&acc)[2][2][4][4]) {
+template <class G>
+G9_DEV void zero_acc(Acc<G>& acc) {
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[q >> 1][q & 1][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < G::FN; ++j) acc[q >> 1][q & 1][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 // Converts the tile to 16-bit (after multiplying by `scale`), stages it in LDS
 // and writes it to C with coalesced 16-byte row chunks, masking rows >= M and
 // columns >= N.  LDS must be free on entry; it is free again on return.
-template <int OUT>
-G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, f32x4 (&acc)[2][2][4][4],
-                       float scale) {
+template <int OUT, class G>
+G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& acc, float scale) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / G::WN, wn = wave % G::WN;
   const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int qm = 0; qm < 2; ++qm)
 #pragma unroll
     for (int qn = 0; qn < 2; ++qn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = qm * 128 + wm * 64 + i * 16 + r16;
-          const int n = qn * 128 + wn * 64 + j * 16 + 4 * g;
+        for (int j = 0; j < G::FN; ++j) {
+          const int m = qm * 128 + wm * G::FM * 16 + i * 16 + r16;
+          const int n = qn * 128 + wn * G::FN * 16 + j * 16 + 4 * g;
           const f32x4 v = acc[qm][qn][i][j] * scale;
           const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
           lds_write8(smem + m * kStageRow + n * 2, h);
         }
   waitcnt<0, 0>();
   barrier();
+  constexpr int kRowsPerPass = G::kThreads / 32;
   const int ch = tid & 31;
   const int row0 = tm * kTile, col = tn * kTile + ch * 8;
   char* cbase = p.c + (size_t)col * 2;
 #pragma unroll 4
-  for (int pass = 0; pass < 32; ++pass) {
-    const int r = pass * 8 + (tid >> 5);
+  for (int pass = 0; pass < kTile / kRowsPerPass; ++pass) {
+    const int r = pass * kRowsPerPass + (tid >> 5);
     const u32x4 d = lds_read16(smem + r * kStageRow + ch * 16);
     const int m = row0 + r;
     if (m < p.M) {
@@ -495,15 +551,15 @@ G9_DEV float epilogue_scale(const GemmParams& p) {
 }
 
 // Data-parallel schedule: one workgroup per 256x256 output tile.
-template <Op OP, int OUT>
-G9_DEV void gemm_dp_4w(const GemmParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes4w];
+template <Op OP, int OUT, class G>
+G9_DEV void gemm_dp(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, tm, tn);
-  f32x4 acc[2][2][4][4];
-  zero_acc(acc);
-  mainloop<OP>(p, smem, tm, tn, 0, p.ns, acc);
-  store_tile<OUT>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+  Acc<G> acc;
+  zero_acc<G>(acc);
+  mainloop<OP, G>(p, smem, tm, tn, 0, p.ns, acc);
+  store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
 }
 
 // ---------------------------------------------------------------------------
@@ -521,8 +577,11 @@ G9_DEV void gemm_dp_4w(const GemmParams& p) {
 // ---------------------------------------------------------------------------
 constexpr u32 kSpinLimit = 1u << 26;
 
+// Index (in f32x4) of a wave's fragment in a tile's partial: the accumulator
+// register layout, so each wave access is a contiguous KiB.
+template <class G>
 G9_DEV int ws_index(int wave, int q, int i, int j, int lane) {
-  return ((wave * 64 + (q * 4 + i) * 4 + j) * 64 + lane);
+  return ((wave * (4 * G::FM * G::FN) + (q * G::FM + i) * G::FN + j) * 64 + lane);
 }
 
 G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
@@ -537,35 +596,35 @@ G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-template <Op OP, int OUT>
+template <Op OP, int OUT, class G>
 G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se) {
   int tm, tn;
   tile_coords(tile, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, 1, p.group_m, tm, tn);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   f32x4* ws = reinterpret_cast<f32x4*>(p.ws) + (size_t)tile * (kTile * kTile / 4);
-  f32x4 acc[2][2][4][4];
+  Acc<G> acc;
   if (sb == 0) {
-    zero_acc(acc);
+    zero_acc<G>(acc);
   } else {
     wait_flag(p, tile, (p.epoch << 16) | (u32)sb);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[q >> 1][q & 1][i][j] = ws[ws_index(wave, q, i, j, lane)];
+        for (int j = 0; j < G::FN; ++j) acc[q >> 1][q & 1][i][j] = ws[ws_index<G>(wave, q, i, j, lane)];
   }
-  mainloop<OP>(p, smem, tm, tn, sb, se, acc);
+  mainloop<OP, G>(p, smem, tm, tn, sb, se, acc);
   if (se == p.ns) {
-    store_tile<OUT>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+    store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
     if (sb != 0 && tid == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ws[ws_index(wave, q, i, j, lane)] = acc[q >> 1][q & 1][i][j];
+        for (int j = 0; j < G::FN; ++j) ws[ws_index<G>(wave, q, i, j, lane)] = acc[q >> 1][q & 1][i][j];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     barrier();
     if (tid == 0)
@@ -573,21 +632,21 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
   }
 }
 
-template <Op OP, int OUT>
-G9_DEV void gemm_sk_4w(const GemmParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes4w];
-  const int G = p.sk_ctas;
+template <Op OP, int OUT, class G>
+G9_DEV void gemm_sk(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  const int G_ = p.sk_ctas;
   // Workgroup ids are dispatched round-robin over the XCDs; give each XCD a
   // contiguous run of ranges so chained neighbours share an L2.
   int cta = blockIdx.x;
   {
     int cm, cn;
-    tile_coords(cta, G, G, 1, p.num_xcds, 1, cm, cn);
+    tile_coords(cta, G_, G_, 1, p.num_xcds, 1, cm, cn);
     cta = cm;
   }
   const long long ipt = p.ns;
   const long long total = (long long)p.tiles_m * p.tiles_n * ipt;
-  const long long base = total / G, rem = total % G;
+  const long long base = total / G_, rem = total % G_;
   const long long u0 = cta * base + min((long long)cta, rem);
   long long u1 = u0 + base + (cta < rem ? 1 : 0);
   while (u1 > u0) {
@@ -595,7 +654,7 @@ G9_DEV void gemm_sk_4w(const GemmParams& p) {
     const long long t0 = (long long)tile * ipt;
     const int sb = (int)(max(u0, t0) - t0);
     const int se = (int)(u1 - t0);
-    sk_segment<OP, OUT>(p, smem, tile, sb, se);
+    sk_segment<OP, OUT, G>(p, smem, tile, sb, se);
     u1 = t0 + sb;
   }
 }

@@ -40,9 +40,10 @@ def test_kernel_names_are_stable_and_unique():
     for dt, out in [(_lib.G9_F16, _lib.G9_F16), (_lib.G9_BF16, _lib.G9_BF16), (_lib.G9_BF8, _lib.G9_F16),
                     (_lib.G9_BF8, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_F16)]:
         for sched in (_lib.G9_SCHED_DP, _lib.G9_SCHED_SK):
-            n = _lib.kernel_name(dt, out, sched, 4)
-            assert n and n.startswith("g9_a") and n not in names
-            names.add(n)
+            for waves in (4, 8):
+                n = _lib.kernel_name(dt, out, sched, waves)
+                assert n and n.startswith("g9_a") and n.endswith(f"_{waves}w") and n not in names
+                names.add(n)
     assert _lib.kernel_name(_lib.G9_F16, _lib.G9_BF16, 0, 4) is None
 
 

@@ -285,3 +285,73 @@ def test_launch_on_side_stream_and_preallocated_c(gpu):
     s.synchronize()
     assert out.data_ptr() == c.data_ptr()
     _check_f16(c, R.a16w16_ref(a.cpu().numpy(), b.cpu().numpy()), K=256, sigma=1.0)
+
+
+# ---------------------------------------------------------------------------
+# 8-wave (inter_wave) kernels: same per-element MFMA sequence as the 4-wave
+# kernels, so their outputs must be bitwise equal.
+# ---------------------------------------------------------------------------
+from gfx950_gluon_tutorials_amd.gemm.inter_wave import a4w4 as iw_a4w4  # noqa: E402
+from gfx950_gluon_tutorials_amd.gemm.inter_wave import a8w8 as iw_a8w8  # noqa: E402
+from gfx950_gluon_tutorials_amd.gemm.inter_wave import a16w16 as iw_a16w16  # noqa: E402
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_inter_wave_exact_fixtures(gpu, schedule):
+    _say(f"8-wave exact fixtures {schedule}")
+    g = np.load(os.path.join(GOLDEN, "a16w16_exact.npz"))
+    a = torch.from_numpy(g["a"]).to(gpu)
+    b_nk = torch.from_numpy(g["b_nk"]).to(gpu)
+    c = torch.empty(a.shape[0], b_nk.shape[0], dtype=torch.float16, device=gpu)
+    iw_a16w16.matmul_kernel_only(a, b_nk, c, schedule=schedule)
+    c2 = iw_a16w16.matmul(a, b_nk.T, schedule=schedule)
+    g8 = np.load(os.path.join(GOLDEN, "a8w8_exact.npz"))
+    a8 = torch.from_numpy(g8["a_codes"]).view(torch.float8_e5m2).to(gpu)
+    b8 = torch.from_numpy(g8["b_codes"]).view(torch.float8_e5m2).to(gpu)
+    c8 = iw_a8w8.matmul(a8, b8.T, schedule=schedule)
+    c8s = torch.empty(a8.shape[0], b8.shape[0], dtype=torch.bfloat16, device=gpu)
+    iw_a8w8.matmul_kernel_only(a8, b8, c8s, a_scale=float(g8["a_scale"]), b_scale=float(g8["b_scale"]),
+                               schedule=schedule)
+    g4 = np.load(os.path.join(GOLDEN, "a4w4_exact.npz"))
+    args4 = [torch.from_numpy(g4[k]).to(gpu) for k in ("a", "b", "a_scales", "b_scales")]
+    c4 = iw_a4w4.matmul(*args4, schedule=schedule)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(c), g["c_f16_bits"])
+    np.testing.assert_array_equal(_bits(c2), g["c_f16_bits"])
+    assert c8.dtype == torch.float16
+    np.testing.assert_array_equal(_bits(c8), g8["c_f16_bits"])
+    np.testing.assert_array_equal(_bits(c8s), g8["c_bf16_scaled_bits"])
+    assert c4.dtype == torch.bfloat16
+    np.testing.assert_array_equal(_bits(c4), g4["c_bf16_bits"])
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16", "bf8", "mxfp4"])
+def test_8wave_bitwise_equals_4wave_at_baseline_size(gpu, kind):
+    _say(f"8-wave == 4-wave {kind} 4096x4096x8192")
+    gen = torch.Generator().manual_seed({"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3}[kind])
+    x = _randn(gen, (4096, 8192))
+    y = _randn(gen, (4096, 8192))
+    if kind in ("fp16", "bf16"):
+        tdt = torch.float16 if kind == "fp16" else torch.bfloat16
+        a, b = (x * 0.1).to(tdt).to(gpu), (y * 0.1).to(tdt).to(gpu)
+        run = lambda w, s: _launch.gemm_a16w16(a, b.T, torch.empty(4096, 4096, dtype=tdt, device=gpu),
+                                               schedule=s, waves=w)
+    elif kind == "bf8":
+        qa, sa = quant.quantize_e5m2(x)
+        qb, sb = quant.quantize_e5m2(y)
+        qa, qb, sa, sb = qa.to(gpu), qb.to(gpu), sa.to(gpu), sb.to(gpu)
+        run = lambda w, s: _launch.gemm_a8w8(qa, qb.T, torch.empty(4096, 4096, dtype=torch.bfloat16, device=gpu),
+                                             a_scale=sa, b_scale=sb, schedule=s, waves=w)
+    else:
+        pa, sa = quant.quantize_mxfp4(x)
+        pb, sb = quant.quantize_mxfp4(y)
+        args = [t.to(gpu) for t in (pa, pb, sa, sb)]
+        run = lambda w, s: _launch.gemm_a4w4(*args, torch.empty(4096, 4096, dtype=torch.bfloat16, device=gpu),
+                                             schedule=s, waves=w)
+    c4 = run(4, "dp")
+    c8 = run(8, "dp")
+    c8sk = run(8, "streamk")
+    torch.cuda.synchronize()
+    _check_streamk_clean(gpu)
+    np.testing.assert_array_equal(_bits(c8), _bits(c4))
+    np.testing.assert_array_equal(_bits(c8sk), _bits(c4))
