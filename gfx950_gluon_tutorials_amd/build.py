@@ -13,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -46,15 +47,32 @@ def hipcc_path() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles the library for gfx950 and returns its path."""
+    """Compiles the library for gfx950, checks its device assembly for MFMA
+    hazards (isa_check) and returns its path.  The library is only replaced
+    when both steps pass."""
+    from . import isa_check
+
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc_path(), *HIPCC_FLAGS, "-I", os.path.join(REPO_DIR, "include"), *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    with tempfile.TemporaryDirectory(prefix="g9build") as work:
+        # -save-temps keeps the device assembly (in the scratch directory)
+        # without a second compilation.
+        cmd = [hipcc_path(), *HIPCC_FLAGS, "-save-temps", "-I", os.path.join(REPO_DIR, "include"), *srcs, "-o", tmp]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True, cwd=work)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        asm = [f for f in os.listdir(work) if f.endswith("gfx950.s")]
+        if len(asm) != len(SOURCES):
+            raise RuntimeError(f"expected {len(SOURCES)} device assembly file(s), found {asm}")
+        bad = []
+        for f in asm:
+            with open(os.path.join(work, f)) as fh:
+                bad += isa_check.check_text(fh.read())
+        if bad:
+            os.unlink(tmp)
+            raise RuntimeError("MFMA hazards in the device code:\n" + "\n".join(bad[:20]))
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

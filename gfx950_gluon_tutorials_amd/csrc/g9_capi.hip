@@ -16,11 +16,19 @@ using namespace g9;
 #define G9_ATTRS(G) \
   __launch_bounds__(G::kThreads) __attribute__((amdgpu_waves_per_eu(G::kWavesPerSimd, G::kWavesPerSimd)))
 
-#define G9_DEFINE(NAME, OP, OUT)                                                                      \
-  extern "C" __global__ G9_ATTRS(Geo4) void NAME##_dp_4w(GemmParams p) { gemm_dp<OP, OUT, Geo4>(p); } \
-  extern "C" __global__ G9_ATTRS(Geo4) void NAME##_sk_4w(GemmParams p) { gemm_sk<OP, OUT, Geo4>(p); } \
-  extern "C" __global__ G9_ATTRS(Geo8) void NAME##_dp_8w(GemmParams p) { gemm_dp<OP, OUT, Geo8>(p); } \
-  extern "C" __global__ G9_ATTRS(Geo8) void NAME##_sk_8w(GemmParams p) { gemm_sk<OP, OUT, Geo8>(p); }
+#define G9_DEFINE(NAME, OP, OUT)                                                                    \
+  using NAME##_g4 = Geo4<kMfmaDim<OP>>;                                                             \
+  using NAME##_g8 = Geo8<kMfmaDim<OP>>;                                                             \
+  extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_dp_4w(GemmParams p) {                       \
+    gemm_dp<OP, OUT, NAME##_g4>(p);                                                                 \
+  }                                                                                                 \
+  extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_sk_4w(GemmParams p) {                       \
+    gemm_sk<OP, OUT, NAME##_g4>(p);                                                                 \
+  }                                                                                                 \
+  extern "C" __global__ G9_ATTRS(NAME##_g8) void NAME##_dp_8w(GemmParams p) {                       \
+    gemm_dp<OP, OUT, NAME##_g8>(p);                                                                 \
+  }                                                                                                 \
+  extern "C" __global__ G9_ATTRS(NAME##_g8) void NAME##_sk_8w(GemmParams p) { gemm_sk<OP, OUT, NAME##_g8>(p); }
 
 G9_DEFINE(g9_a16w16_f16, Op::F16, OUT_F16)
 G9_DEFINE(g9_a16w16_bf16, Op::BF16, OUT_BF16)

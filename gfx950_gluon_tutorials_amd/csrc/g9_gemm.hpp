@@ -38,6 +38,7 @@
 // out as coalesced 16-byte row chunks.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 
 #include "g9_common.hpp"
@@ -79,12 +80,20 @@ constexpr int kLdsBytes = 139264;           // 128 KiB operands + 8 KiB scales
 static_assert(kTile * kStageRow <= kLdsBytes, "staging must fit");
 
 // Wave geometry: NW waves as WM x WN; per quadrant a wave owns FM x FN MFMA
-// 16x16 fragments (FM*16 rows of A, FN*16 rows of B).
-template <int NW_, int WM_, int WN_>
+// fragments of MD x MD outputs (FM*MD rows of A, FN*MD rows of B).  A
+// fragment's 64 lanes split into NG = 64/MD lane groups: lane l works on row
+// l % MD and lane group l / MD, and holds NC = 8/NG of the eight 16-byte chunks
+// of that row in a stage.
+template <int NW_, int WM_, int WN_, int MD_>
 struct Geo {
-  static constexpr int NW = NW_, WM = WM_, WN = WN_;
+  static constexpr int NW = NW_, WM = WM_, WN = WN_, MD = MD_;
+  static_assert(MD == 16 || MD == 32, "MFMA fragments are 16x16 or 32x32");
   static constexpr int kThreads = 64 * NW;
-  static constexpr int FM = 128 / 16 / WM, FN = 128 / 16 / WN;
+  static constexpr int FM = 128 / WM / MD, FN = 128 / WN / MD;
+  static constexpr int FMAX = FM > FN ? FM : FN;
+  static constexpr int NG = 64 / MD;        // lane groups per fragment
+  static constexpr int NC = 8 / NG;         // 16-byte chunks per lane per fragment per stage
+  static constexpr int NB = MD * MD / 256;  // 4-float accumulator quads per fragment
   static constexpr int kDmaRows = 128 / NW;        // rows of each sub-buffer one wave loads
   static constexpr int kDmaPerSub = kDmaRows / 8;  // 16-byte DMAs per wave per sub-buffer
   // FP4 scale DMA: one dword per lane, kDmaRows rows of 8 bytes per wave, so
@@ -93,134 +102,221 @@ struct Geo {
   // pack the 8-wave share into fewer bytes per lane).
   static constexpr int kScaleLanes = 2 * kDmaRows;
   static constexpr int kWavesPerSimd = NW / 4;
+  // Row chunk held as the lane's chunk r by lane group gi.  The same map is
+  // used for A and B, so it only permutes K inside a stage.
+  //   MD 16: chunk 4r + gi.  16x16 MFMA step r takes K chunk 4r..4r+3 from
+  //          lane groups 0..3, which is the natural K order for FP16/BF16/FP4;
+  //          BF8 feeds chunks r = 0, 1 to one MFMA (a K permutation), which
+  //          keeps the read pattern of the 16-bit types, free of bank
+  //          conflicts (the contiguous chunks 2gi, 2gi + 1 measured 2-way
+  //          conflicts).
+  //   MD 32: chunk 4gi + r.  Lane group gi holds K chunks 4gi..4gi+3, so an
+  //          FP4 lane's four E8M0 scales (groups 4gi..4gi+3) are one aligned
+  //          dword of its row's eight scale bytes, read without a byte
+  //          shuffle.
+  static constexpr int chunk(int r, int gi) { return MD == 16 ? 4 * r + gi : 4 * gi + r; }
 };
-using Geo4 = Geo<4, 2, 2>;
-using Geo8 = Geo<8, 2, 4>;
+template <int MD>
+using Geo4 = Geo<4, 2, 2, MD>;
+template <int MD>
+using Geo8 = Geo<8, 2, 4, MD>;
 
-// Operand fragment of one 16-row slice for one stage: 32 bytes per lane, plus
-// (FP4) the lane's 8 raw scale bytes of the stage.
+// MFMA fragment size per operand type (build-time choice, 16 or 32).  32x32
+// MFMAs are twice as long as the 16x16 ones, which leaves more issue slots per
+// MFMA for the LDS reads, DMAs and barrier (a block-scaled 16x16x128 MFMA
+// leaves only one) and halves the number of block-scale loads: the loop runs
+// at 97-98% MFMA occupancy for FP16/BF8 and 87% for MXFP4, against 90%, 96%
+// and 73% with 16x16.  But the chip is power-limited in this kernel, the
+// 32x32 MFMAs draw more energy per FLOP, and the sustained clock drops by more
+// than the occupancy gains: measured back to back on the same MI355X at
+// 4096x4096x8192, 16x16 is 6% faster for FP16, 5% for BF8 and 1.5% for MXFP4.
+#ifndef G9_MD_F16
+#define G9_MD_F16 16
+#endif
+#ifndef G9_MD_BF8
+#define G9_MD_BF8 16
+#endif
+#ifndef G9_MD_FP4
+#define G9_MD_FP4 16
+#endif
+
+// Operand fragment of one MD-row slice for one stage: NC chunks of 16 bytes
+// per lane, plus (FP4) the lane's E8M0 scales.
+template <int NC>
 struct Frag {
-  u32x4 c[2];
-  u32x2 sc;  // FP4: the lane's 8 raw E8M0 bytes of the stage (groups 0..7)
-  u32 sp;    // FP4: byte 0 = scale of group g (step 0), byte 1 = group 4+g (step 1)
+  u32x4 c[NC];
+  u32x2 sc;  // FP4, MD 16: the lane's 8 raw E8M0 bytes of the stage (groups 0..7)
+  u32 sp;    // FP4: byte e = scale of the lane's data in MFMA step e
 };
 
 template <Op OP>
 struct OpInfo {
   static constexpr bool kScaled = OP == Op::FP4;
-  static constexpr int kSub = OP == Op::BF8 ? 1 : 2;  // MFMAs per fragment pair per stage
-  // The two 16-byte chunks (of the row's eight) lane group g reads per stage:
-  // chunks g and 4+g.  For FP16/BF16 and FP4 they feed MFMA step e; BF8 feeds
-  // both to one 16x16x128 MFMA, so its lane group g holds K bytes 16g..16g+15
-  // and 64+16g..64+16g+15 instead of a contiguous 32 -- the same K
-  // permutation for A and B, so the dot product is unchanged, and the LDS read
-  // pattern is the FP16 one, which measures free of bank conflicts (the
-  // contiguous 2g, 2g+1 assignment measured 2-way conflicts).
-  static G9_DEV int chunk(int e, int g) { return 4 * e + g; }
+  static constexpr int kChunksPerMfma = OP == Op::BF8 ? 2 : 1;  // 16-byte chunks per lane per MFMA
 };
+template <Op OP>
+constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : G9_MD_F16;
 
 template <Op OP, class G>
 struct Shape {
-  static constexpr int NM = G::FM * G::FN * OpInfo<OP>::kSub;  // MFMAs per wave per region
+  static constexpr int KS = G::NC / OpInfo<OP>::kChunksPerMfma;  // MFMA steps per stage
+  static constexpr int NM = G::FM * G::FN * KS;                  // MFMAs per wave per region
   static constexpr int kDmaPerRegion = G::kDmaPerSub + (OpInfo<OP>::kScaled ? 1 : 0);
 };
+
+template <class G>
+using accv = std::conditional_t<G::MD == 16, f32x4, f32x16>;
+template <class G>
+using FragSet = Frag<G::NC>[G::FMAX];
+
+// Four consecutive accumulator registers 4B..4B+3 of a fragment.
+template <int B, class V>
+G9_DEV f32x4 get_quad(const V& v) {
+  if constexpr (sizeof(V) == sizeof(f32x4))
+    return v;
+  else
+    return __builtin_shufflevector(v, v, 4 * B, 4 * B + 1, 4 * B + 2, 4 * B + 3);
+}
+// A fragment's accumulators from NB quads (p[0], p[64], ... : one quad per
+// 64-lane row of a partial tile).
+template <class V>
+G9_DEV V load_quads(const f32x4* p) {
+  if constexpr (sizeof(V) == sizeof(f32x4)) {
+    return p[0];
+  } else {
+    const f32x4 a = p[0], b = p[64], c = p[128], d = p[192];
+    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7),
+                                   __builtin_shufflevector(c, d, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2, 3, 4, 5, 6, 7, 8,
+                                   9, 10, 11, 12, 13, 14, 15);
+  }
+}
 
 // LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
 constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s) * kSubBytes; }
 constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; }
 
-// One MFMA of step H of the stage on a (B fragment, A fragment) pair, written
-// as inline assembly with the accumulator tied in place ("+a").  The compiler
+// Block-scaled MFMA step E: byte E of each scale VGPR is the scale
+// (op_sel and op_sel_hi bit 0 of the scale operands select the byte).
+#define G9_MFMA_SCALED(SHAPE)                                                                          \
+  do {                                                                                                 \
+    if constexpr (E == 0)                                                                              \
+      asm("v_mfma_scale_f32_" SHAPE "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"   \
+          : "+a"(acc)                                                                                  \
+          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
+    else if constexpr (E == 1)                                                                         \
+      asm("v_mfma_scale_f32_" SHAPE                                                                    \
+          "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"              \
+          : "+a"(acc)                                                                                  \
+          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
+    else if constexpr (E == 2)                                                                         \
+      asm("v_mfma_scale_f32_" SHAPE "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,1,0] cbsz:4 blgp:4"   \
+          : "+a"(acc)                                                                                  \
+          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
+    else                                                                                               \
+      asm("v_mfma_scale_f32_" SHAPE                                                                    \
+          "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[1,1,0] cbsz:4 blgp:4"              \
+          : "+a"(acc)                                                                                  \
+          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
+  } while (0)
+
+// MFMA step E of the stage on a (B fragment, A fragment) pair, written as
+// inline assembly with the accumulator tied in place ("+a").  The compiler
 // selects an untied MFMA form for the builtins and then renames every
 // accumulator chain across the AGPRs, which costs hundreds of AGPR copies per
 // loop iteration; the tied form keeps each chain in its registers.  The
 // hazard recognizer does not see through inline assembly, so the callers
 // insert the MFMA-to-VALU wait states themselves (see mfma_drain) and never
-// feed an MFMA from a VALU result written within a few cycles.
-// FP4 takes the lane's two E8M0 scales from the fragments' `sp`.
-template <Op OP, int H>
-G9_DEV void mma(f32x4& acc, const Frag& bx, const Frag& ay) {
-  if constexpr (OP == Op::F16) {
-    asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[H]), "v"(ay.c[H]));
-  } else if constexpr (OP == Op::BF16) {
-    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[H]), "v"(ay.c[H]));
-  } else if constexpr (OP == Op::BF8) {
-    // e5m2 x e5m2 (format code 1), 32 bytes per lane; no block scales (the
-    // per-tensor scales are applied in the epilogue).
-    const i32x8 x = __builtin_bit_cast(i32x8, __builtin_shufflevector(bx.c[0], bx.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
-    const i32x8 y = __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[0], ay.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
-    asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
+// feed an MFMA from a VALU result written within a few cycles.  (Back-to-back
+// MFMAs accumulating into the same registers need no wait states.)
+template <Op OP, class G, int E>
+G9_DEV void mma(accv<G>& acc, const Frag<G::NC>& bx, const Frag<G::NC>& ay) {
+  if constexpr (G::MD == 16) {
+    if constexpr (OP == Op::F16) {
+      asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[E]), "v"(ay.c[E]));
+    } else if constexpr (OP == Op::BF16) {
+      asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[E]), "v"(ay.c[E]));
+    } else if constexpr (OP == Op::BF8) {
+      // e5m2 x e5m2 (format code 1), 32 bytes per lane; no block scales (the
+      // per-tensor scales are applied in the epilogue).
+      const i32x8 x = __builtin_bit_cast(i32x8, __builtin_shufflevector(bx.c[0], bx.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      const i32x8 y = __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[0], ay.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
+    } else {
+      // e2m1 x e2m1 (format code 4), 16 bytes per lane.
+      G9_MFMA_SCALED("16x16x128");
+    }
   } else {
-    // e2m1 x e2m1 (format code 4), 16 bytes per lane.  Byte H of the scale
-    // registers is scale group 4H+g of the lane's row (op_sel picks it).
-    if constexpr (H == 0)
-      asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"
-          : "+a"(acc)
-          : "v"(bx.c[0]), "v"(ay.c[0]), "v"(bx.sp), "v"(ay.sp));
-    else
-      asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"
-          : "+a"(acc)
-          : "v"(bx.c[1]), "v"(ay.c[1]), "v"(bx.sp), "v"(ay.sp));
+    if constexpr (OP == Op::F16) {
+      asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[E]), "v"(ay.c[E]));
+    } else if constexpr (OP == Op::BF16) {
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[E]), "v"(ay.c[E]));
+    } else if constexpr (OP == Op::BF8) {
+      const i32x8 x =
+          __builtin_bit_cast(i32x8, __builtin_shufflevector(bx.c[2 * E], bx.c[2 * E + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+      const i32x8 y =
+          __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[2 * E], ay.c[2 * E + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+      asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
+    } else {
+      G9_MFMA_SCALED("32x32x64");
+    }
   }
 }
 
 // Wait states between the last inline-assembly MFMA writing an accumulator and
-// the first VALU/memory access to it (the longest gfx950 MFMA here has 8
-// passes; 3 x s_nop 7 covers it with margin).
+// the first VALU/memory access to it (the longest gfx950 MFMA here, the 32x32
+// BF8 one, needs 20).
 G9_DEV void mfma_drain() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Where, inside a region of NM MFMAs, the other instructions are issued (they
-// go right after MFMA number k).  The first kPre MFMAs are issued before the
-// region's s_barrier (their operands are already in registers), so the MFMA
-// pipe stays busy while the barrier resolves; LDS reads and DMAs follow the
-// barrier.  The region's NR 16-byte LDS reads come first, spread over a window
-// of W slots, so the region-closing lgkmcnt(0) finds them complete; the DMAs
-// are spread over the whole region.  FP4 gathers the scale bytes of the set it
-// just read at slot kPermSlot, after its reads and well before the next
-// region's MFMAs read the results.
+template <int N, class F>
+G9_DEV void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) { (f(std::integral_constant<int, I>{}), ...); }(
+      std::make_integer_sequence<int, N>{});
+}
+
+// Where, inside a region of NM MFMAs, the other instructions are issued.  The
+// first kPre MFMAs are issued before the region's s_barrier (their operands
+// are already in registers), so the MFMA pipe stays busy while the barrier
+// resolves; everything else follows the barrier, placed after MFMA kPre + q
+// for q in [0, NQ).  The region's NR 16-byte LDS reads come first, spread over
+// a window of W slots, so the region-closing lgkmcnt(0) finds them complete;
+// the DMAs are spread over the whole region.  FP4 reads one scale word per
+// fragment after the first reads; with 16x16 fragments it then gathers the
+// bytes each MFMA step needs at slot kPermQ, after its reads and well before
+// the next region's MFMAs read the results.
 template <Op OP, class G, int NF>
 struct Slots {
-  using SH = Shape<OP, G>;
-  static constexpr int NM = SH::NM;
-  static constexpr int kPre = (OP == Op::BF8 || G::NW == 8) ? 1 : 2;
-  static constexpr int NQ = NM - kPre;  // slots after the barrier
-  static constexpr int NR = 2 * NF;     // 16-byte reads of the set loaded in this region
+  static constexpr int NM = Shape<OP, G>::NM;
+  static constexpr int kPre = (G::MD == 32 || OP == Op::BF8 || G::NW == 8) ? 1 : 2;
+  static constexpr int NQ = NM - kPre;
+  static constexpr int NR = G::NC * NF;
   static constexpr int W = NQ < (NR > NQ / 2 ? NR : NQ / 2) ? NQ : (NR > NQ / 2 ? NR : NQ / 2);
-  // reads issued after MFMA k: [first_read(k), first_read(k + 1))
-  static constexpr int first_read(int k) {
-    const int q = k - kPre;
-    if (q <= 0) return 0;
-    if (q >= W) return NR;
-    return (q * NR + W - 1) / W;
-  }
-  static constexpr int kLastReadSlot = kPre + W - 1;
-  static constexpr int kRead8Step = (W + NF - 1) / NF;
-  static constexpr int read8(int k) {  // FP4 scale-row read number, or -1
-    const int q = k - kPre - 1;
-    return (OpInfo<OP>::kScaled && q >= 0 && q % kRead8Step == 0 && q / kRead8Step < NF) ? q / kRead8Step : -1;
-  }
-  static constexpr int dma16(int k) {  // 16-byte DMA number, or -1
-    const int q = k - kPre;
-    constexpr int D = G::kDmaPerSub;
-    constexpr int step = (NQ - 1) / D;
-    return (q >= 1 && (q - 1) % step == 0 && (q - 1) / step < D) ? (q - 1) / step : -1;
-  }
-  static constexpr bool dma_scale(int k) { return OpInfo<OP>::kScaled && k - kPre == 5; }
-  static constexpr int kLastRead8Slot = kPre + 1 + (NF - 1) * kRead8Step;
-  static constexpr int kAfterReads = (kLastReadSlot > kLastRead8Slot ? kLastReadSlot : kLastRead8Slot) + 3;
-  static constexpr int kPermSlot =
-      (kAfterReads > NM - 8 ? kAfterReads : NM - 8) < NM - 1 ? (kAfterReads > NM - 8 ? kAfterReads : NM - 8) : NM - 1;
-  static_assert(!OpInfo<OP>::kScaled || kLastRead8Slot < NM, "scale reads must fit the region");
+  static constexpr int read_q(int R) { return R * W / NR; }
+  static constexpr int kScaleStep = (W + NF - 1) / NF;
+  static constexpr int scale_q(int F) { return 1 + F * kScaleStep; }
+  static constexpr int D = G::kDmaPerSub;
+  static constexpr int dma_q(int J) { return NQ == 1 ? 0 : 1 + J * (NQ - 1) / D; }
+  static constexpr int kScaleDmaQ = NQ > 5 ? 5 : NQ - 1;
+  static constexpr int kLastQ = (read_q(NR - 1) > scale_q(NF - 1) ? read_q(NR - 1) : scale_q(NF - 1)) + 3;
+  static constexpr int kPermQ = (kLastQ > NQ - 8 ? kLastQ : NQ - 8) < NQ - 1 ? (kLastQ > NQ - 8 ? kLastQ : NQ - 8)
+                                                                              : NQ - 1;
+  static_assert(NQ >= 1, "a region needs an MFMA after its barrier");
+  static_assert(!OpInfo<OP>::kScaled || scale_q(NF - 1) < NQ, "scale reads must fit the region");
 };
 
 // Keeps a value in a register the compiler cannot see through, so constant
 // parts of LDS addresses stay in the instruction's offset field.
 G9_DEV u32 opaque(u32 x) {
   asm volatile("" : "+v"(x));
+  return x;
+}
+// Same for a wave-uniform value, which also keeps the compiler from hoisting
+// everything derived from it out of the loop.
+G9_DEV u32 opaque_s(u32 x) {
+  asm volatile("" : "+s"(x));
   return x;
 }
 
@@ -234,21 +330,30 @@ struct Pipe {
   rsrc_t rSA[2], rSB[2];    // FP4 scale half-tiles
   u32 vA[D], vB[D];         // DMA offsets of the wave's 1-KiB runs
   u32 vSA, vSB;             // FP4 scale DMA offsets
-  u32 bA[2], bB[2];         // LDS read bases of the lane's two chunks (A at 0, B at 64 KiB)
+  u32 bA[G::NC], bB[G::NC];  // LDS read bases of the lane's chunks (A at 0, B at 64 KiB)
   u32 bSA, bSB;             // FP4 LDS read bases of the lane's scale row (at 128 KiB)
-  u32 sel;                  // FP4 scale byte selector
+  u32 sel;                  // FP4, MD 16: scale byte selector
   u32 lds0;                 // LDS address of the shared buffer
+  u32 mrow;                 // LDS address of the wave's rows in sub-buffer A0, slot 0
+  u32 msc;                  // LDS address of the wave's rows in scale sub-buffer A0, slot 0
   int wave;
   int s_end;                // first stage not to load
 
   G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int end) {
-    s_end = end;
+    // Tile coordinates are wave-uniform; saying so keeps the buffer resources
+    // in SGPRs (a resource the compiler thinks divergent is issued through a
+    // per-lane "waterfall" loop around every DMA).
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
+    s_end = __builtin_amdgcn_readfirstlane(end);
     lds0 = (u32)(uintptr_t)to_lds(smem);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    mrow = lds0 + (u32)wave * (G::kDmaRows * kRowBytes);
+    msc = lds0 + kScaleBase + (u32)wave * (G::kDmaRows * 8);
     const int wm = wave / G::WN, wn = wave % G::WN;
-    const int g = lane >> 4, r16 = lane & 15;
+    const int gi = lane / G::MD, rr = lane % G::MD;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int ra = tm * kTile + h * 128, rb = tn * kTile + h * 128;
@@ -268,21 +373,27 @@ struct Pipe {
       vA[j] = (u32)row * p.lda + ch * 16;
       vB[j] = (u32)row * p.ldb + ch * 16;
     }
-    const int sw = r16 >> 1;
+    // Fragment row bases are multiples of 16, so the swizzle of the lane's
+    // row depends on rr only.
+    const int sw = (rr >> 1) & 7;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int slot = I::chunk(e, g) ^ sw;
-      bA[e] = opaque(lds0 + (u32)(wm * G::FM * 16 + r16) * kRowBytes + slot * 16);
-      bB[e] = opaque(lds0 + 65536u + (u32)(wn * G::FN * 16 + r16) * kRowBytes + slot * 16);
+    for (int c = 0; c < G::NC; ++c) {
+      const int slot = G::chunk(c, gi) ^ sw;
+      bA[c] = opaque(lds0 + (u32)(wm * G::FM * G::MD + rr) * kRowBytes + slot * 16);
+      bB[c] = opaque(lds0 + 65536u + (u32)(wn * G::FN * G::MD + rr) * kRowBytes + slot * 16);
     }
     if constexpr (I::kScaled) {
       // Each wave loads kDmaRows scale rows of 8 bytes, two dwords per row.
       const int row = G::kDmaRows * wave + (lane >> 1);
       vSA = (u32)row * p.ldsa + (lane & 1) * 4;
       vSB = (u32)row * p.ldsb + (lane & 1) * 4;
-      bSA = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * 16 + r16) * 8);
-      bSB = opaque(lds0 + kScaleBase + (u32)(wn * G::FN * 16 + r16) * 8);
-      sel = (u32)g | ((u32)(4 + g) << 8) | 0x0c0c0000u;
+      // MD 16 reads the row's 8 scale bytes and picks groups gi and 4 + gi
+      // (byte 0x0c of a v_perm selector yields zero); MD 32 reads the dword
+      // of groups 4gi..4gi+3 directly.
+      const u32 word = G::MD == 32 ? 4u * gi : 0u;
+      bSA = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * 8 + word);
+      bSB = opaque(lds0 + kScaleBase + (u32)(wn * G::FN * G::MD + rr) * 8 + word);
+      sel = (u32)gi | ((u32)(4 + gi) << 8) | 0x0c0c0000u;
     } else {
       sel = 0;
     }
@@ -292,14 +403,17 @@ struct Pipe {
   G9_DEV rsrc_t src_sc(int X, bool live) const { return live ? (X < 2 ? rSA[X & 1] : rSB[X & 1]) : rZ; }
 
   // 16-byte DMA number J (rows 8J..8J+7 of the wave's kDmaRows) of sub-buffer X.
+  // `mb` is mrow, passed through opaque_s once per region: the 32 distinct
+  // LDS destinations then cost one s_add each instead of 32 SGPRs held for
+  // the whole loop.
   template <int X, int SLOT, int J>
-  G9_DEV void dma_rows(rsrc_t r, u32 soff) const {
-    const u32 dst = lds0 + sub_off(X, SLOT) + (u32)wave * (G::kDmaRows * kRowBytes) + J * 1024;
+  G9_DEV void dma_rows(rsrc_t r, u32 soff, u32 mb) const {
+    const u32 dst = mb + sub_off(X, SLOT) + J * 1024;
     dma16(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
   }
   template <int X, int SLOT>
-  G9_DEV void dma_scales(rsrc_t r, u32 soff) const {
-    const u32 dst = lds0 + scale_off(X, SLOT) + (u32)wave * (G::kDmaRows * 8);
+  G9_DEV void dma_scales(rsrc_t r, u32 soff, u32 mb) const {
+    const u32 dst = mb + (scale_off(X, SLOT) - kScaleBase);
     if constexpr (G::kScaleLanes == 64) {
       dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
     } else {
@@ -309,19 +423,23 @@ struct Pipe {
     }
   }
 
-  // 16-byte LDS read number R (fragment R/2, chunk R%2) of sub-buffer X.
+  // 16-byte LDS read number R (fragment R / NC, chunk R % NC) of sub-buffer X.
   template <int X, int SLOT, int R>
-  G9_DEV void read_chunk(Frag (&f)[4]) const {
+  G9_DEV void read_chunk(FragSet<G>& f) const {
+    constexpr int NC = G::NC;
     constexpr int region = X < 2 ? 0 : 65536;
-    constexpr int imm = sub_off(X, SLOT) - region + (R / 2) * 2048;
-    const u32 base = X < 2 ? bA[R % 2] : bB[R % 2];
-    f[R / 2].c[R % 2] = *(const G9_LDS u32x4*)(uintptr_t)(base + imm);
+    constexpr int imm = sub_off(X, SLOT) - region + (R / NC) * G::MD * kRowBytes;
+    const u32 base = X < 2 ? bA[R % NC] : bB[R % NC];
+    f[R / NC].c[R % NC] = *(const G9_LDS u32x4*)(uintptr_t)(base + imm);
   }
   template <int X, int SLOT, int F>
-  G9_DEV void read_scales(Frag (&f)[4]) const {
-    constexpr int imm = scale_off(X, SLOT) - kScaleBase + F * 128;
+  G9_DEV void read_scales(FragSet<G>& f) const {
+    constexpr int imm = scale_off(X, SLOT) - kScaleBase + F * G::MD * 8;
     const u32 base = X < 2 ? bSA : bSB;
-    f[F].sc = *(const G9_LDS u32x2*)(uintptr_t)(base + imm);
+    if constexpr (G::MD == 16)
+      f[F].sc = *(const G9_LDS u32x2*)(uintptr_t)(base + imm);
+    else
+      f[F].sp = *(const G9_LDS u32*)(uintptr_t)(base + imm);
   }
 
   // Whole-set variants for the prologue.
@@ -330,22 +448,22 @@ struct Pipe {
     const bool live = stage < s_end;
     const rsrc_t r = src(X, live);
     const u32 soff = (u32)stage * kRowBytes;
-    [&]<int... J>(std::integer_sequence<int, J...>) { (dma_rows<X, SLOT, J>(r, soff), ...); }(
+    [&]<int... J>(std::integer_sequence<int, J...>) { (dma_rows<X, SLOT, J>(r, soff, mrow), ...); }(
         std::make_integer_sequence<int, D>{});
-    if constexpr (I::kScaled) dma_scales<X, SLOT>(src_sc(X, live), (u32)stage * 8);
+    if constexpr (I::kScaled) dma_scales<X, SLOT>(src_sc(X, live), (u32)stage * 8, msc);
   }
   template <int X, int SLOT>
-  G9_DEV void load(Frag (&f)[4]) const {
+  G9_DEV void load(FragSet<G>& f) const {
     constexpr int NF = X < 2 ? G::FM : G::FN;
     [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
-        std::make_integer_sequence<int, 2 * NF>{});
+        std::make_integer_sequence<int, G::NC * NF>{});
     if constexpr (I::kScaled) {
       [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SLOT, F>(f), ...); }(
           std::make_integer_sequence<int, NF>{});
     }
   }
   template <int X>
-  G9_DEV void gather_scales(Frag (&f)[4]) const {
+  G9_DEV void gather_scales(FragSet<G>& f) const {
     constexpr int NF = X < 2 ? G::FM : G::FN;
 #pragma unroll
     for (int i = 0; i < NF; ++i) f[i].sp = __builtin_amdgcn_perm(f[i].sc.y, f[i].sc.x, sel);
@@ -354,30 +472,65 @@ struct Pipe {
 
 // Per-quadrant accumulators of one wave.
 template <class G>
-using QAcc = f32x4[G::FM][G::FN];
+using QAcc = accv<G>[G::FM][G::FN];
 template <class G>
-using Acc = f32x4[2][2][G::FM][G::FN];
+using Acc = accv<G>[2][2][G::FM][G::FN];
+
+// Puts every accumulator in an AGPR at this point.  Called where a tile's
+// accumulation starts, so the values the main loop's MFMAs tie to AGPRs
+// arrive there from every path (zeroing or a stream-K partial) and the
+// register allocator has no reason to stage them in VGPRs.
+template <class G>
+G9_DEV void pin_acc(Acc<G>& acc) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FN; ++j) asm volatile("" : "+a"(acc[q >> 1][q & 1][i][j]));
+}
+
+// Waits out the last MFMAs, then redefines every accumulator after the wait.
+// Ends every path out of an MFMA stream: anything the compiler later
+// generates to read the accumulators (copies at a control-flow join, spills,
+// the epilogue) then reads the redefined values and so comes after the wait
+// states, which it would not insert itself after inline-assembly MFMAs.
+// isa_check.py verifies the built kernels for exactly this.
+template <class G>
+G9_DEV void settle_acc(Acc<G>& acc) {
+  mfma_drain();
+  pin_acc<G>(acc);
+}
 
 // Slot K of a region: MFMA number K (step-major: step, A fragment, B
 // fragment), then whatever the slot table puts after it, then a hard
 // scheduling fence (the MFMAs are inline assembly, which the scheduler's
 // instruction-class masks do not cover, so only a full fence pins the order).
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int K>
-G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, QAcc<G>& acc,
-                        const Frag (&bx)[4], const Frag (&ay)[4], Frag (&nxt)[4]) {
+G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, u32 mb, QAcc<G>& acc,
+                        const FragSet<G>& bx, const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
-  constexpr int h = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j = K % G::FN;
-  mma<OP, h>(acc[i][j], bx[j], ay[i]);
-  [&]<int... R>(std::integer_sequence<int, R...>) {
-    (P.template read_chunk<RX, RSLOT, S::first_read(K) + R>(nxt), ...);
-  }(std::make_integer_sequence<int, S::first_read(K + 1) - S::first_read(K)>{});
-  if constexpr (S::read8(K) >= 0) P.template read_scales<RX, RSLOT, S::read8(K)>(nxt);
-  if constexpr (S::dma16(K) >= 0) P.template dma_rows<DX, DSLOT, S::dma16(K)>(r, soff);
-  if constexpr (S::dma_scale(K)) P.template dma_scales<DX, DSLOT>(rs, soff_sc);
-  if constexpr (OpInfo<OP>::kScaled && K == S::kPermSlot) {
-    waitcnt<63, 0>();
-    P.template gather_scales<RX>(nxt);
+  constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j = K % G::FN;
+  mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
+  constexpr int q = K - S::kPre;
+  if constexpr (q >= 0) {
+    static_for<S::NR>([&](auto R) {
+      if constexpr (S::read_q(decltype(R)::value) == q) P.template read_chunk<RX, RSLOT, decltype(R)::value>(nxt);
+    });
+    if constexpr (OpInfo<OP>::kScaled) {
+      static_for<NF>([&](auto F) {
+        if constexpr (S::scale_q(decltype(F)::value) == q) P.template read_scales<RX, RSLOT, decltype(F)::value>(nxt);
+      });
+    }
+    static_for<S::D>([&](auto J) {
+      if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
+    });
+    if constexpr (OpInfo<OP>::kScaled && q == S::kScaleDmaQ) P.template dma_scales<DX, DSLOT>(rs, soff_sc, opaque_s(P.msc));
+    if constexpr (OpInfo<OP>::kScaled && G::MD == 16 && q == S::kPermQ) {
+      waitcnt<63, 0>();
+      P.template gather_scales<RX>(nxt);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -392,8 +545,8 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT>
-G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const Frag (&bx)[4], const Frag (&ay)[4],
-                   Frag (&nxt)[4]) {
+G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
+                   FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
   __builtin_amdgcn_sched_barrier(0);
@@ -403,20 +556,21 @@ G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const Frag (&bx)[
   rsrc_t rs = r;
   if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
   const u32 soff = (u32)ds * kRowBytes, soff_sc = (u32)ds * 8;
+  const u32 mb = opaque_s(P.mrow);
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, mb, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::kPre>{});
   barrier();
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, mb, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
 // Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
 // they are consumed the next stage's B0 fragments go to y as well.
 template <Op OP, class G>
-G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, Frag (&at)[4], Frag (&ab)[4], Frag (&x)[4],
-                       Frag (&y)[4]) {
+G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
+                       FragSet<G>& y) {
   region<OP, G, 3, 0, 2, 0>(P, s + 2, acc[0][0], x, at, y);
   region<OP, G, 1, 0, 3, 0>(P, s + 2, acc[0][1], y, at, ab);
   region<OP, G, 0, 1, 1, 0>(P, s + 2, acc[1][1], y, ab, at);
@@ -426,8 +580,8 @@ G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, Frag (&at)[4], 
 // Odd stage (slot 1): B0 fragments in y; B1 fragments go to x, then the next
 // stage's B0 fragments.
 template <Op OP, class G>
-G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, Frag (&at)[4], Frag (&ab)[4], Frag (&x)[4],
-                      Frag (&y)[4]) {
+G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
+                      FragSet<G>& y) {
   region<OP, G, 3, 1, 2, 1>(P, s + 2, acc[0][0], y, at, x);
   region<OP, G, 1, 1, 3, 1>(P, s + 2, acc[0][1], x, at, ab);
   region<OP, G, 0, 0, 1, 1>(P, s + 2, acc[1][1], x, ab, at);
@@ -454,11 +608,11 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   // A0 slot 0 with stage s0+2.
   waitcnt<6 * DQ, 0>();
   barrier();
-  Frag at[4], ab[4], x[4], y[4];
+  FragSet<G> at, ab, x, y;
   P.template load<0, 0>(at);
   P.template load<2, 0>(x);
   waitcnt<6 * DQ, 0>();
-  if constexpr (OpInfo<OP>::kScaled) {
+  if constexpr (OpInfo<OP>::kScaled && G::MD == 16) {
     P.template gather_scales<0>(at);
     P.template gather_scales<2>(x);
   }
@@ -475,8 +629,11 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
     stage_even(P, s, acc, at, ab, x, y);
     stage_odd(P, s + 1, acc, at, ab, x, y);
   }
-  if ((s1 - s0) & 1) stage_even(P, s, acc, at, ab, x, y);
-  mfma_drain();
+  settle_acc<G>(acc);
+  if ((s1 - s0) & 1) {
+    stage_even(P, s, acc, at, ab, x, y);
+    settle_acc<G>(acc);
+  }
   waitcnt<0, 0>();
   barrier();
 }
@@ -488,7 +645,7 @@ G9_DEV void zero_acc(Acc<G>& acc) {
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-      for (int j = 0; j < G::FN; ++j) acc[q >> 1][q & 1][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < G::FN; ++j) acc[q >> 1][q & 1][i][j] = accv<G>{};
 }
 
 // Converts the tile to 16-bit (after multiplying by `scale`), stages it in LDS
@@ -498,7 +655,7 @@ template <int OUT, class G>
 G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& acc, float scale) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
-  const int r16 = lane & 15, g = lane >> 4;
+  const int rr = lane % G::MD, gi = lane / G::MD;
 #pragma unroll
   for (int qm = 0; qm < 2; ++qm)
 #pragma unroll
@@ -506,13 +663,15 @@ G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& 
 #pragma unroll
       for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < G::FN; ++j) {
-          const int m = qm * 128 + wm * G::FM * 16 + i * 16 + r16;
-          const int n = qn * 128 + wn * G::FN * 16 + j * 16 + 4 * g;
-          const f32x4 v = acc[qm][qn][i][j] * scale;
-          const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
-          lds_write8(smem + m * kStageRow + n * 2, h);
-        }
+        for (int j = 0; j < G::FN; ++j)
+          static_for<G::NB>([&](auto B) {
+            constexpr int b = decltype(B)::value;
+            const int m = qm * 128 + wm * G::FM * G::MD + i * G::MD + rr;
+            const int n = qn * 128 + wn * G::FN * G::MD + j * G::MD + 4 * G::NG * b + 4 * gi;
+            const f32x4 v = get_quad<b>(acc[qm][qn][i][j]) * scale;
+            const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
+            lds_write8(smem + m * kStageRow + n * 2, h);
+          });
   waitcnt<0, 0>();
   barrier();
   constexpr int kRowsPerPass = G::kThreads / 32;
@@ -558,6 +717,7 @@ G9_DEV void gemm_dp(const GemmParams& p) {
   tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, tm, tn);
   Acc<G> acc;
   zero_acc<G>(acc);
+  pin_acc<G>(acc);
   mainloop<OP, G>(p, smem, tm, tn, 0, p.ns, acc);
   store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
 }
@@ -580,13 +740,17 @@ constexpr u32 kSpinLimit = 1u << 26;
 // Index (in f32x4) of a wave's fragment in a tile's partial: the accumulator
 // register layout, so each wave access is a contiguous KiB.
 template <class G>
-G9_DEV int ws_index(int wave, int q, int i, int j, int lane) {
-  return ((wave * (4 * G::FM * G::FN) + (q * G::FM + i) * G::FN + j) * 64 + lane);
+G9_DEV int ws_index(int wave, int q, int i, int j, int b, int lane) {
+  return (((wave * (4 * G::FM * G::FN) + (q * G::FM + i) * G::FN + j) * G::NB + b) * 64 + lane);
 }
 
+// The flag is read once per wave (readfirstlane), so the loop and everything
+// after it stay wave-uniform in the compiler's eyes; a per-lane exit condition
+// would make the buffer resources built after it look divergent.
 G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
   u32 spins = 0;
-  while (__hip_atomic_load(p.flags + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
+  while (__builtin_amdgcn_readfirstlane(
+             __hip_atomic_load(p.flags + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != want) {
     __builtin_amdgcn_s_sleep(2);
     if (++spins > kSpinLimit) {
       __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -612,8 +776,10 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
 #pragma unroll
       for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < G::FN; ++j) acc[q >> 1][q & 1][i][j] = ws[ws_index<G>(wave, q, i, j, lane)];
+        for (int j = 0; j < G::FN; ++j)
+          acc[q >> 1][q & 1][i][j] = load_quads<accv<G>>(ws + ws_index<G>(wave, q, i, j, 0, lane));
   }
+  pin_acc<G>(acc);
   mainloop<OP, G>(p, smem, tm, tn, sb, se, acc);
   if (se == p.ns) {
     store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
@@ -624,7 +790,11 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
 #pragma unroll
       for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < G::FN; ++j) ws[ws_index<G>(wave, q, i, j, lane)] = acc[q >> 1][q & 1][i][j];
+        for (int j = 0; j < G::FN; ++j)
+          static_for<G::NB>([&](auto B) {
+            constexpr int b = decltype(B)::value;
+            ws[ws_index<G>(wave, q, i, j, b, lane)] = get_quad<b>(acc[q >> 1][q & 1][i][j]);
+          });
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     barrier();
     if (tid == 0)
@@ -650,10 +820,10 @@ G9_DEV void gemm_sk(const GemmParams& p) {
   const long long u0 = cta * base + min((long long)cta, rem);
   long long u1 = u0 + base + (cta < rem ? 1 : 0);
   while (u1 > u0) {
-    const int tile = (int)((u1 - 1) / ipt);
+    const int tile = __builtin_amdgcn_readfirstlane((int)((u1 - 1) / ipt));
     const long long t0 = (long long)tile * ipt;
-    const int sb = (int)(max(u0, t0) - t0);
-    const int se = (int)(u1 - t0);
+    const int sb = __builtin_amdgcn_readfirstlane((int)(max(u0, t0) - t0));
+    const int se = __builtin_amdgcn_readfirstlane((int)(u1 - t0));
     sk_segment<OP, OUT, G>(p, smem, tile, sb, se);
     u1 = t0 + sb;
   }
