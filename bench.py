@@ -37,6 +37,10 @@ REFERENCE_TFLOPS = {"fp16": 1608.0, "bf8": 3215.0, "mxfp4": 4986.0}
 # 8-wave: kernels/gemm/inter_wave/a16w16/README.md:120, kernels/gemm/inter_wave/a8w8/README.md:61,
 # kernels/gemm/inter_wave/a4w4/README.md:17.
 REFERENCE_TFLOPS_8W = {"fp16": 1478.0, "bf8": 2949.0, "mxfp4": 4479.0}
+# BF16 and the headline-K shapes (4-wave, 8-wave): scripts/plot_perf_summary.py:53-58.
+REFERENCE_TFLOPS["bf16"] = 1696.0
+REFERENCE_TFLOPS_8W["bf16"] = 1573.6
+HEADLINE_K = {"bf8": (16384, 3476.0, 3131.1), "mxfp4": (32768, 5804.0, 5195.9)}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -45,7 +49,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--dtypes", default="fp16,bf8,mxfp4", help="comma list of fp16,bf16,bf8,mxfp4")
+    p.add_argument("--dtypes", default="fp16,bf16,bf8,mxfp4", help="comma list of fp16,bf16,bf8,mxfp4")
+    p.add_argument("--headline-k", type=int, default=1,
+                   help="also time bf8 at K=16384 and mxfp4 at K=32768, the reference's headline shapes")
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
     p.add_argument("--waves", default="4,8", help="wave schedules to time: 4 (1 wave/SIMD), 8 (2 waves/SIMD)")
     p.add_argument("--cpu-baseline", type=int, default=1)
@@ -246,6 +252,14 @@ def summarize_rocpd(path: str) -> None:
                 print(f"{name[:48]:48s} grid={grid} dispatches={n} median_us={st.median(g['dur']):.2f}  {vals}")
 
 
+def streamk_fixups(tiles: int, stages: int, ctas: int) -> int:
+    """Partial tiles handed from one stream-K workgroup to the next: the CTA
+    range boundaries (c*base + min(c, rem)) that fall inside a tile."""
+    total = tiles * stages
+    base, rem = divmod(total, ctas)
+    return sum(1 for c in range(1, ctas) if (c * base + min(c, rem)) % stages)
+
+
 def load_traffic(key: str):
     try:
         with open(TRAFFIC_FILE) as f:
@@ -274,26 +288,32 @@ def main():
     seeds = {"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3}
     results = {}
     waves = [int(w) for w in args.waves.split(",") if w]
-    for dt in dtypes:
-        for w in waves:
-            nsets = max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, M, N, K)))
-            launch = make_case(dt, M, N, K, seeds[dt], dev, nsets, w)
-            ms = time_case(launch, args.steps, args.warmup)
-            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-            key = dt if w == 4 else f"{dt}_8w"
-            results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
-                            "reference_tflops": REFERENCE_TFLOPS.get(dt) if w == 4 else REFERENCE_TFLOPS_8W.get(dt),
-                            "rotating_sets": nsets, "waves": w}
-            msg = f"# {key}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak"
-            if args.serialized:
-                ms_s = time_serialized(launch)
-                tf_s = 2.0 * M * N * K / (ms_s * 1e-3) / 1e12
-                results[key]["serialized_tflops"] = round(tf_s, 2)
-                results[key]["serialized_ms"] = round(ms_s, 5)
-                msg += f"  | serialized (reference protocol) {ms_s * 1e3:.1f} us {tf_s:.1f} TFLOPS"
-            print(msg, flush=True)
-            del launch
-            torch.cuda.empty_cache()
+    cases = [(dt, K, w, REFERENCE_TFLOPS.get(dt) if w == 4 else REFERENCE_TFLOPS_8W.get(dt), args.rotate_mb)
+             for dt in dtypes for w in waves]
+    if args.headline_k and not args.only:
+        for dt, (kk, r4, r8) in HEADLINE_K.items():
+            if dt in dtypes:
+                cases += [(dt, kk, w, r4 if w == 4 else r8, max(args.rotate_mb, 2048)) for w in waves]
+    for dt, kk, w, ref, rotate_mb in cases:
+        nsets = max(2, -(-rotate_mb * 2**20 // set_bytes(dt, M, N, kk)))
+        launch = make_case(dt, M, N, kk, seeds[dt], dev, nsets, w)
+        ms = time_case(launch, args.steps, args.warmup)
+        tf = 2.0 * M * N * kk / (ms * 1e-3) / 1e12
+        key = dt + ("" if kk == K else f"_k{kk}") + ("" if w == 4 else "_8w")
+        results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
+                        "reference_tflops": ref, "K": kk, "rotating_sets": nsets, "waves": w}
+        msg = f"# {key}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak"
+        if args.serialized:
+            ms_s = time_serialized(launch)
+            tf_s = 2.0 * M * N * kk / (ms_s * 1e-3) / 1e12
+            results[key]["serialized_tflops"] = round(tf_s, 2)
+            results[key]["serialized_ms"] = round(ms_s, 5)
+            msg += f"  | serialized (reference protocol) {ms_s * 1e3:.1f} us {tf_s:.1f} TFLOPS"
+        if ref:
+            msg += f"  | reference {ref:.0f}"
+        print(msg, flush=True)
+        del launch
+        torch.cuda.empty_cache()
     sk = {}
     if args.streamk and not args.only:
         for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192)]:
@@ -301,9 +321,17 @@ def main():
             ms_dp = time_case(launch, max(10, args.steps // 4), 3, "dp")
             ms_sk = time_case(launch, max(10, args.steps // 4), 3, "streamk")
             flop = 2.0 * m * n * k
+            from gfx950_gluon_tutorials_amd import _lib
+
+            tiles, stages = -(-m // 256) * -(-n // 256), k // 64
+            ctas = min(tiles * stages, _lib.load().g9_streamk_workgroups())
+            fix = streamk_fixups(tiles, stages, ctas)
             sk[f"{m}x{n}x{k}"] = {"dp_tflops": round(flop / ms_dp / 1e9, 2), "sk_tflops": round(flop / ms_sk / 1e9, 2),
-                                  "dp_ms": round(ms_dp, 5), "sk_ms": round(ms_sk, 5)}
-            print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f} TFLOPS", flush=True)
+                                  "dp_ms": round(ms_dp, 5), "sk_ms": round(ms_sk, 5), "sk_workgroups": ctas,
+                                  "fixups": fix, "fixup_bytes": fix * 2 * 256 * 256 * 4}
+            print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f} TFLOPS  "
+                  f"({ctas} workgroups, {fix} partial-tile handoffs = {fix * 0.5:.0f} MiB fp32 written+read)",
+                  flush=True)
             del launch
             torch.cuda.empty_cache()
     if args.copy_mb:

@@ -20,6 +20,9 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libg9gemm.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# The same kernels with per-workgroup phase stamps (-DG9_TIMING), for
+# profiling.py; never loaded by the wrappers unless G9_LIBRARY points at it.
+LIB_TIMING_PATH = os.path.join(PKG_DIR, "libg9gemm_timing.so")
 SOURCES = ["g9_capi.hip"]
 HEADERS = ["g9_common.hpp", "g9_gemm.hpp"]
 
@@ -46,18 +49,24 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, timing: bool = False) -> str:
     """Compiles the library for gfx950, checks its device assembly for MFMA
     hazards (isa_check) and returns its path.  The library is only replaced
-    when both steps pass."""
+    when both steps pass; the kernels' register and scratch use is written
+    next to it (``<lib>.resources.json``).  ``timing`` builds the stamped
+    variant instead."""
+    import json
+
     from . import isa_check
 
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
+    lib_path = LIB_TIMING_PATH if timing else LIB_PATH
+    flags = HIPCC_FLAGS + (["-DG9_TIMING"] if timing else [])
+    tmp = lib_path + ".tmp"
     with tempfile.TemporaryDirectory(prefix="g9build") as work:
         # -save-temps keeps the device assembly (in the scratch directory)
         # without a second compilation.
-        cmd = [hipcc_path(), *HIPCC_FLAGS, "-save-temps", "-I", os.path.join(REPO_DIR, "include"), *srcs, "-o", tmp]
+        cmd = [hipcc_path(), *flags, "-save-temps", "-I", os.path.join(REPO_DIR, "include"), *srcs, "-o", tmp]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True, cwd=work)
@@ -66,16 +75,20 @@ def build(verbose: bool = False) -> str:
         asm = [f for f in os.listdir(work) if f.endswith("gfx950.s")]
         if len(asm) != len(SOURCES):
             raise RuntimeError(f"expected {len(SOURCES)} device assembly file(s), found {asm}")
-        bad = []
+        bad, resources = [], []
         for f in asm:
             with open(os.path.join(work, f)) as fh:
-                bad += isa_check.check_text(fh.read())
+                text = fh.read()
+            bad += isa_check.check_text(text)
+            resources += isa_check.resource_table(text)
         if bad:
             os.unlink(tmp)
             raise RuntimeError("MFMA hazards in the device code:\n" + "\n".join(bad[:20]))
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    with open(lib_path + ".resources.json", "w") as fh:
+        json.dump(resources, fh, indent=1)
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timing="--timing" in sys.argv))

@@ -319,3 +319,14 @@ int g9_streamk_workgroups(void) { return cu_count(); }
 int g9_version(void) { return 100; }
 
 }  // extern "C"
+
+#ifdef G9_TIMING
+#include "../../include/gfx950_gemm_timing.h"
+extern "C" int g9_timing_read(void* host, size_t bytes) {
+  if (bytes > sizeof(g9::g9_timing_buf)) return G9_ERR_SHAPE;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g9::g9_timing_buf), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}
+extern "C" int g9_timing_capacity(void) { return g9::kTimingTiles; }
+#endif

@@ -45,6 +45,30 @@
 
 namespace g9 {
 
+// Optional phase stamps (build with -DG9_TIMING; see profiling.py): thread 0
+// of each data-parallel workgroup records s_memtime (shader clock) and
+// s_memrealtime (100 MHz) at kernel entry, main-loop start, main-loop end and
+// kernel end, for the first kTimingTiles workgroups.  Each stamp waits only
+// for its own scalar reads, so the pipeline around it is unchanged.  Compiled
+// to nothing in the regular build.
+#ifdef G9_TIMING
+constexpr int kTimingTiles = 16384;
+__device__ unsigned long long g9_timing_buf[kTimingTiles * 8];
+G9_DEV void timing_stamp(int slot) {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memtime();
+  const unsigned long long r = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));  // lgkmcnt(0) only
+  if (threadIdx.x == 0 && blockIdx.x < kTimingTiles) {
+    g9_timing_buf[blockIdx.x * 8 + slot * 2] = t;
+    g9_timing_buf[blockIdx.x * 8 + slot * 2 + 1] = r;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+#else
+G9_DEV void timing_stamp(int) {}
+#endif
+
 enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3 };
 enum : int { OUT_F16 = 0, OUT_BF16 = 1 };
 
@@ -591,7 +615,8 @@ G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, 
 // Accumulates stages [s0, s1) of tile (tm, tn) into acc.  Leaves every DMA
 // complete and the workgroup synchronised, so LDS is free on return.
 template <Op OP, class G>
-G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, Acc<G>& acc) {
+G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, Acc<G>& acc,
+                     bool stamp = false) {
   constexpr int DQ = Shape<OP, G>::kDmaPerRegion;
   Pipe<OP, G> P;
   P.init(p, smem, tm, tn, s1);
@@ -623,6 +648,7 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   mfma_drain();
   // Two stages per iteration (the B registers swap roles between them), then
   // a peeled even stage when the count is odd.
+  if (stamp) timing_stamp(1);
   int s = s0;
   const int pairs = (s1 - s0) >> 1;
   for (int it = 0; it < pairs; ++it, s += 2) {
@@ -716,10 +742,13 @@ G9_DEV void gemm_dp(const GemmParams& p) {
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, tm, tn);
   Acc<G> acc;
+  timing_stamp(0);
   zero_acc<G>(acc);
   pin_acc<G>(acc);
-  mainloop<OP, G>(p, smem, tm, tn, 0, p.ns, acc);
+  mainloop<OP, G>(p, smem, tm, tn, 0, p.ns, acc, true);
+  timing_stamp(2);
   store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+  timing_stamp(3);
 }
 
 // ---------------------------------------------------------------------------

@@ -238,6 +238,32 @@ def check_text(asm: str) -> list[str]:
     return violations
 
 
+def resource_table(asm: str) -> list[dict]:
+    """Per-kernel register, scratch and LDS use from the code-object metadata
+    of an assembly listing (the figures the reference reads from its own
+    builds: VGPR, AGPR and spill counts)."""
+    rows = []
+    for blk in asm.split("  - .agpr_count:")[1:]:
+        def field(name, cast=int):
+            m = re.search(rf"\.{name}:\s+(\S+)", blk)
+            return cast(m.group(1)) if m else None
+
+        name = field("name", str)
+        if name is None or name.startswith("_Z"):
+            continue
+        rows.append({
+            "kernel": name,
+            "agpr": int(re.match(r"\s*(\d+)", blk).group(1)),
+            "vgpr_total": field("vgpr_count"),
+            "sgpr": field("sgpr_count"),
+            "vgpr_spill": field("vgpr_spill_count"),
+            "sgpr_spill": field("sgpr_spill_count"),
+            "scratch_bytes": field("private_segment_fixed_size"),
+            "lds_bytes": field("group_segment_fixed_size"),
+        })
+    return sorted(rows, key=lambda r: r["kernel"])
+
+
 def main(argv: list[str]) -> int:
     bad = []
     for path in argv:

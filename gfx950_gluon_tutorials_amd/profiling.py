@@ -1,0 +1,162 @@
+"""Phase timing and main-loop MFMA efficiency of the data-parallel kernels.
+
+The reference measures "MFMA efficiency" -- the fraction of main-loop cycles
+the SIMD's matrix pipe is busy -- from ATT thread traces of one wave
+(``scripts/process_json.py:52-235``, ``docs/mfma_efficiency.md``).  The ATT
+decoder is not available here, so this build records the phases directly: the
+timing library (``libg9gemm_timing.so``, the same kernels compiled with
+``-DG9_TIMING``) has thread 0 of every workgroup stamp the shader clock and the
+100 MHz clock at kernel entry, main-loop start, main-loop end and kernel end.
+
+Per workgroup (all its SIMDs run the same schedule):
+
+* prologue = loop start - entry, loop = loop end - loop start, epilogue =
+  end - loop end, in shader-clock cycles;
+* ideal loop cycles = stages x 2048: a 256x256 tile stage is
+  256*256*K_stage*2 FLOP spread over 4 SIMDs at 1024 (FP16/BF16, K_stage 64),
+  2048 (BF8, K_stage 128) or 4096 (MXFP4, K_stage 256) FLOP/clock/SIMD, which
+  is 2048 cycles for every type and for both wave counts;
+* MFMA efficiency = ideal / loop (per SIMD, the figure the reference quotes);
+* clock = shader cycles / 100 MHz ticks over the kernel.
+
+Usage (on a GPU box, after ``python -m gfx950_gluon_tutorials_amd.build
+--timing``)::
+
+    python -m gfx950_gluon_tutorials_amd.profiling --dtypes fp16,bf8,mxfp4 --K 8192 --waves 4,8
+
+The stamps cost a few scalar instructions per workgroup; the main loop is
+compiled unchanged.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+
+import numpy as np
+
+CYCLES_PER_STAGE = 2048
+STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256}
+REALTIME_HZ = 100e6
+
+
+def phase_stats(stamps: np.ndarray, stages: int) -> dict:
+    """Summarises raw stamps (workgroups x 8 uint64: clock/realtime pairs at
+    entry, loop start, loop end, end) into medians and spreads."""
+    d = np.asarray(stamps, dtype=np.int64).reshape(-1, 8)
+    t = d[:, 0::2]
+    r = d[:, 1::2]
+    pro = t[:, 1] - t[:, 0]
+    loop = t[:, 2] - t[:, 1]
+    epi = t[:, 3] - t[:, 2]
+    ticks = r[:, 3] - r[:, 0]
+    if (ticks <= 0).any() or (loop <= 0).any():
+        raise ValueError("stamps are not increasing: was the last launch a DP launch of the timing build?")
+    clock = (t[:, 3] - t[:, 0]) / (ticks / REALTIME_HZ)
+    ideal = stages * CYCLES_PER_STAGE
+    loop_med = float(np.median(loop))
+    return {
+        "workgroups": int(d.shape[0]),
+        "stages": stages,
+        "clock_ghz": round(float(np.median(clock)) / 1e9, 4),
+        "span_us": round(float(r[:, 3].max() - r[:, 0].min()) / REALTIME_HZ * 1e6, 2),
+        "start_skew_us": round(float(r[:, 0].max() - r[:, 0].min()) / REALTIME_HZ * 1e6, 3),
+        "prologue_cycles": int(np.median(pro)),
+        "loop_cycles": int(loop_med),
+        "loop_cycles_min": int(loop.min()),
+        "loop_cycles_max": int(loop.max()),
+        "epilogue_cycles": int(np.median(epi)),
+        "ideal_loop_cycles": ideal,
+        "mfma_efficiency": round(ideal / loop_med, 4),
+        "loop_fraction": round(loop_med / float(np.median(t[:, 3] - t[:, 0])), 4),
+    }
+
+
+def _inputs(dtype: str, M: int, N: int, K: int, dev, seed: int = 0):
+    import torch
+
+    from . import quant
+
+    g = torch.Generator().manual_seed(seed)
+    if dtype in ("fp16", "bf16"):
+        tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+        a = (torch.randn(M, K, generator=g) * 0.1).to(tdt).to(dev)
+        b = (torch.randn(N, K, generator=g) * 0.1).to(tdt).to(dev)
+        return a, b.T, torch.empty(M, N, dtype=tdt, device=dev)
+    if dtype == "bf8":
+        qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=g).to(dev))
+        qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=g).to(dev))
+        return qa, qb.T, torch.empty(M, N, dtype=torch.bfloat16, device=dev), sa, sb
+    pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=g).to(dev))
+    pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=g).to(dev))
+    return pa, pb, sa, sb, torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+
+def measure(dtype: str, M: int, N: int, K: int, waves: int, warmup: int = 20) -> dict:
+    import ctypes
+
+    import torch
+
+    from . import _lib
+    from .gemm import _launch
+
+    lib = _lib.load()
+    if not hasattr(lib, "g9_timing_read"):
+        raise RuntimeError(f"{_lib.LIB_PATH} is not the timing build (python -m gfx950_gluon_tutorials_amd.build --timing)")
+    lib.g9_timing_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.g9_timing_capacity.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    x = _inputs(dtype, M, N, K, dev)
+    if dtype in ("fp16", "bf16"):
+        run = lambda: _launch.gemm_a16w16(x[0], x[1], x[2], waves=waves)
+    elif dtype == "bf8":
+        run = lambda: _launch.gemm_a8w8(x[0], x[1], x[2], a_scale=x[3], b_scale=x[4], waves=waves)
+    else:
+        run = lambda: _launch.gemm_a4w4(x[0], x[1], x[2], x[3], x[4], waves=waves)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    run()
+    torch.cuda.synchronize()
+    tiles = -(-M // 256) * -(-N // 256)
+    n = min(tiles, lib.g9_timing_capacity())
+    buf = np.zeros(n * 8, dtype=np.uint64)
+    _lib.check(lib.g9_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_timing_read")
+    out = phase_stats(buf, K // STAGE_K[dtype])
+    out.update({"dtype": dtype, "M": M, "N": N, "K": K, "waves": waves})
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--dtypes", default="fp16,bf8,mxfp4")
+    ap.add_argument("--M", type=int, default=4096)
+    ap.add_argument("--N", type=int, default=4096)
+    ap.add_argument("--K", default="8192", help="comma-separated list")
+    ap.add_argument("--waves", default="4")
+    ap.add_argument("--json", help="also write the results to this file")
+    args = ap.parse_args(argv)
+    results = []
+    for dt in args.dtypes.split(","):
+        for K in (int(k) for k in args.K.split(",")):
+            for w in (int(v) for v in args.waves.split(",")):
+                r = measure(dt, args.M, args.N, K, w)
+                results.append(r)
+                print(f"{dt:6s} {args.M}x{args.N}x{K} waves={w}: MFMA eff {r['mfma_efficiency']:.3f}  "
+                      f"clock {r['clock_ghz']:.3f} GHz  span {r['span_us']:.1f} us  prologue {r['prologue_cycles']}  "
+                      f"loop {r['loop_cycles']} (ideal {r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles",
+                      flush=True)
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(results, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    if not os.environ.get("G9_LIBRARY"):
+        from . import build as _b
+
+        os.environ["G9_LIBRARY"] = _b.LIB_TIMING_PATH
+    sys.exit(main())

@@ -27,6 +27,27 @@ def test_library_exports_every_declared_function():
         assert hasattr(lib, n), f"{n} declared in gfx950_gemm.h but not exported"
 
 
+TIMING_HEADER = os.path.join(os.path.dirname(HEADER), "gfx950_gemm_timing.h")
+
+
+def test_timing_build_exports_its_header_and_the_regular_one_does_not():
+    from gfx950_gluon_tutorials_amd import build as _b
+
+    text = open(TIMING_HEADER).read()
+    names = sorted(set(re.findall(r"^\s*\w+\s*\*?\s*(g9_\w+)\s*\(", text, flags=re.M)))
+    assert names == ["g9_timing_capacity", "g9_timing_read"]
+    regular = _lib.load()
+    for n in names:
+        assert not hasattr(regular, n), f"{n} leaked into the regular library"
+    if not os.path.exists(_b.LIB_TIMING_PATH):
+        pytest.skip("timing library not built")
+    timing = ctypes.CDLL(_b.LIB_TIMING_PATH)
+    for n in names + declared_functions():
+        assert hasattr(timing, n), f"{n} missing from the timing library"
+    timing.g9_timing_capacity.restype = ctypes.c_int
+    assert timing.g9_timing_capacity() >= 256
+
+
 def test_version_and_status_strings():
     lib = _lib.load()
     assert lib.g9_version() >= 100

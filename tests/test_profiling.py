@@ -1,0 +1,41 @@
+"""Phase accounting of profiling.py on synthetic stamps (the GPU side only
+fills the buffer; the arithmetic is checked here)."""
+
+import numpy as np
+import pytest
+
+from gfx950_gluon_tutorials_amd import profiling
+
+
+def _stamps(pro, loop, epi, clock_hz=1.5e9, start_ticks=1000, n=4):
+    rows = []
+    for w in range(n):
+        t0 = 10_000 + 7 * w
+        t = [t0, t0 + pro, t0 + pro + loop + 10 * w, t0 + pro + loop + 10 * w + epi]
+        r = [start_ticks + w + int(round((x - t0) / clock_hz * profiling.REALTIME_HZ)) for x in t]
+        rows.append([v for pair in zip(t, r) for v in pair])
+    return np.array(rows, dtype=np.uint64)
+
+
+def test_efficiency_and_clock():
+    stages = 128
+    ideal = stages * profiling.CYCLES_PER_STAGE
+    s = profiling.phase_stats(_stamps(3000, int(ideal / 0.9), 8000), stages)
+    assert s["ideal_loop_cycles"] == ideal
+    assert abs(s["mfma_efficiency"] - 0.9) < 1e-3
+    assert abs(s["clock_ghz"] - 1.5) < 0.01
+    assert s["prologue_cycles"] == 3000 and s["epilogue_cycles"] == 8000
+    assert s["loop_cycles_max"] - s["loop_cycles_min"] == 30
+
+
+def test_cycles_per_stage_matches_the_mfma_rates():
+    # 256x256 tile, K per stage, over 4 SIMDs at the dtype's FLOP/clock/SIMD.
+    for dt, flop_per_clk in (("fp16", 1024), ("bf16", 1024), ("bf8", 2048), ("mxfp4", 4096)):
+        assert 256 * 256 * profiling.STAGE_K[dt] * 2 / (4 * flop_per_clk) == profiling.CYCLES_PER_STAGE
+
+
+def test_rejects_stamps_from_another_launch():
+    bad = _stamps(3000, 100000, 8000)
+    bad[:, 4] = bad[:, 2] - 5  # loop end before loop start
+    with pytest.raises(ValueError):
+        profiling.phase_stats(bad, 64)
