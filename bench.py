@@ -7,8 +7,11 @@ A "step" is one GEMM launch over one set of synthetic operands already
 resident in HBM.  The operands rotate over several sets (>= 512 MiB in total)
 so every launch starts with cold caches, as in the reference's protocol
 (kernels/gemm/intra_wave/a16w16/bench.py:190-241).  Timing: W untimed warm-up
-launches, then K launches bracketed by synchronize + HIP events on the launch
-stream; ms_per_step is the average launch time and TFLOPS = 2*M*N*K / t.
+launches, continued until --settle-ms of load has passed (the chip's clocks
+need a few hundred ms of load to settle; the reference's protocol likewise
+discards 900 of 1000 dispatches), then K launches bracketed by synchronize +
+HIP events on the launch stream; ms_per_step is the average launch time and
+TFLOPS = 2*M*N*K / t.
 
 The JSON line also carries the roofline of the dominant kernel (MFMA-bound:
 achieved TFLOP/s vs the published dense peak) with the HBM traffic per launch
@@ -47,8 +50,11 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--settle-ms", type=float, default=600.0,
+                   help="keep warming up until this much time has passed (the MI355X's clocks take a few "
+                        "hundred ms of load to settle; timed launches before that run up to 15%% slower)")
     p.add_argument("--dtypes", default="fp16,bf16,bf8,mxfp4", help="comma list of fp16,bf16,bf8,mxfp4")
     p.add_argument("--headline-k", type=int, default=1,
                    help="also time bf8 at K=16384 and mxfp4 at K=32768, the reference's headline shapes")
@@ -134,12 +140,22 @@ def set_bytes(dtype, M, N, K):
     return (M * K + N * K) // 2 + (M + N) * K // 32 + 2 * M * N
 
 
-def time_case(launch, steps, warmup, schedule="dp"):
+def time_case(launch, steps, warmup, schedule="dp", settle_s=0.0):
+    """Average ms per launch of `steps` back-to-back launches, after `warmup`
+    untimed launches that continue (in blocks of 20) until `settle_s` seconds
+    of warm-up have passed."""
     import torch
 
+    t0 = time.perf_counter()
     for i in range(warmup):
         launch(i, schedule)
     torch.cuda.synchronize()
+    i = warmup
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(20):
+            launch(i, schedule)
+            i += 1
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -297,7 +313,7 @@ def main():
     for dt, kk, w, ref, rotate_mb in cases:
         nsets = max(2, -(-rotate_mb * 2**20 // set_bytes(dt, M, N, kk)))
         launch = make_case(dt, M, N, kk, seeds[dt], dev, nsets, w)
-        ms = time_case(launch, args.steps, args.warmup)
+        ms = time_case(launch, args.steps, args.warmup, settle_s=args.settle_ms / 1e3)
         tf = 2.0 * M * N * kk / (ms * 1e-3) / 1e12
         key = dt + ("" if kk == K else f"_k{kk}") + ("" if w == 4 else "_8w")
         results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
@@ -318,8 +334,8 @@ def main():
     if args.streamk and not args.only:
         for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192)]:
             launch = make_case("fp16", m, n, k, 4, dev, 2)
-            ms_dp = time_case(launch, max(10, args.steps // 4), 3, "dp")
-            ms_sk = time_case(launch, max(10, args.steps // 4), 3, "streamk")
+            ms_dp = time_case(launch, max(10, args.steps // 2), args.warmup, "dp", args.settle_ms / 2e3)
+            ms_sk = time_case(launch, max(10, args.steps // 2), args.warmup, "streamk", args.settle_ms / 2e3)
             flop = 2.0 * m * n * k
             from gfx950_gluon_tutorials_amd import _lib
 
@@ -345,6 +361,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": r["ms"],
         "higher_is_better": True,
         "scaling": "weak",

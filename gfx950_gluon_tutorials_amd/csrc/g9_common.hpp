@@ -35,14 +35,24 @@ G9_DEV rsrc_t make_rsrc(const void* base, u32 bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// One LDS-DMA of 16 bytes per lane: lane i writes lds + 16*i (the whole wave
-// writes one contiguous KiB starting at `lds`), reading global base+voff+soff.
+// Cache-policy bits of the operand DMAs (gfx950 CPol: bit 0 sc0, bit 1 nt,
+// bit 4 sc1); a build option.
+#ifndef G9_DMA_CPOL
+#define G9_DMA_CPOL 0
+#endif
+
+// One LDS-DMA of 16 bytes per lane: lane i writes lds + IMM + 16*i (the whole
+// wave writes one contiguous KiB), reading global base + voff + soff + IMM.
+// The instruction's immediate offset moves the global and the LDS address
+// alike, so DMAs IMM bytes apart in both can share one M0 (the LDS base).
+template <int IMM = 0>
 G9_DEV void dma16(rsrc_t r, G9_LDS void* lds, u32 voff, u32 soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, (int)voff, (int)soff, 0, 0);
+  static_assert(IMM >= 0 && IMM < 4096, "MUBUF immediate offsets are 12 bits");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, (int)voff, (int)soff, IMM, G9_DMA_CPOL);
 }
 // Same with 4 bytes per lane (a wave writes 256 contiguous bytes).
 G9_DEV void dma4(rsrc_t r, G9_LDS void* lds, u32 voff, u32 soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, (int)voff, (int)soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, (int)voff, (int)soff, 0, G9_DMA_CPOL);
 }
 
 // s_waitcnt with vmcnt(VM) and lgkmcnt(LG); expcnt is left unconstrained.

@@ -390,12 +390,18 @@ struct Pipe {
       }
     }
     rZ = make_rsrc(p.a, 0);
+    // DMA j of a sub-buffer covers rows 8j..8j+7 of the wave's share and is
+    // issued with immediate offset 1024j, which advances the LDS destination
+    // by 1024j as well, so the four DMAs of a region share one M0.  The global
+    // offset gives the 1024j back (row >= 8j and lda >= 128, so it stays
+    // non-negative); the buffer range check sees voffset + soffset + imm, i.e.
+    // the row's true offset, so rows past the valid count still read zero.
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
       const int ch = (lane & 7) ^ ((row >> 1) & 7);
-      vA[j] = (u32)row * p.lda + ch * 16;
-      vB[j] = (u32)row * p.ldb + ch * 16;
+      vA[j] = (u32)row * p.lda + ch * 16 - 1024u * j;
+      vB[j] = (u32)row * p.ldb + ch * 16 - 1024u * j;
     }
     // Fragment row bases are multiples of 16, so the swizzle of the lane's
     // row depends on rr only.
@@ -427,13 +433,14 @@ struct Pipe {
   G9_DEV rsrc_t src_sc(int X, bool live) const { return live ? (X < 2 ? rSA[X & 1] : rSB[X & 1]) : rZ; }
 
   // 16-byte DMA number J (rows 8J..8J+7 of the wave's kDmaRows) of sub-buffer X.
-  // `mb` is mrow, passed through opaque_s once per region: the 32 distinct
-  // LDS destinations then cost one s_add each instead of 32 SGPRs held for
-  // the whole loop.
+  // `mb` is mrow, passed through opaque_s once per region: the 8 distinct
+  // LDS destinations (sub-buffer x slot) then cost one s_add per region
+  // instead of SGPRs held for the whole loop; J moves the destination through
+  // the immediate offset.
   template <int X, int SLOT, int J>
   G9_DEV void dma_rows(rsrc_t r, u32 soff, u32 mb) const {
-    const u32 dst = mb + sub_off(X, SLOT) + J * 1024;
-    dma16(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
+    const u32 dst = mb + sub_off(X, SLOT);
+    dma16<J * 1024>(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
   }
   template <int X, int SLOT>
   G9_DEV void dma_scales(rsrc_t r, u32 soff, u32 mb) const {
@@ -568,14 +575,19 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32
 //                                             wave done reading the sub-buffer
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
-template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT>
+//
+// LIVE: the caller guarantees stage `ds` exists, so the operand resources are
+// used directly; otherwise a stage past the end reads from the empty resource
+// (zeros, no memory traffic) and the per-region choice costs a few SALU
+// selects, which the main loop avoids by running LIVE until its last pairs.
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, bool LIVE>
 G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
                    FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
   __builtin_amdgcn_sched_barrier(0);
   waitcnt<6 * Shape<OP, G>::kDmaPerRegion, 0>();
-  const bool live = ds < P.s_end;
+  const bool live = LIVE || ds < P.s_end;
   const rsrc_t r = P.src(DX, live);
   rsrc_t rs = r;
   if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
@@ -592,24 +604,24 @@ G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const FragSet<G>&
 
 // Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
 // they are consumed the next stage's B0 fragments go to y as well.
-template <Op OP, class G>
+template <Op OP, class G, bool LIVE>
 G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
                        FragSet<G>& y) {
-  region<OP, G, 3, 0, 2, 0>(P, s + 2, acc[0][0], x, at, y);
-  region<OP, G, 1, 0, 3, 0>(P, s + 2, acc[0][1], y, at, ab);
-  region<OP, G, 0, 1, 1, 0>(P, s + 2, acc[1][1], y, ab, at);
-  region<OP, G, 2, 1, 0, 1>(P, s + 3, acc[1][0], x, ab, y);
+  region<OP, G, 3, 0, 2, 0, LIVE>(P, s + 2, acc[0][0], x, at, y);
+  region<OP, G, 1, 0, 3, 0, LIVE>(P, s + 2, acc[0][1], y, at, ab);
+  region<OP, G, 0, 1, 1, 0, LIVE>(P, s + 2, acc[1][1], y, ab, at);
+  region<OP, G, 2, 1, 0, 1, LIVE>(P, s + 3, acc[1][0], x, ab, y);
 }
 
 // Odd stage (slot 1): B0 fragments in y; B1 fragments go to x, then the next
 // stage's B0 fragments.
-template <Op OP, class G>
+template <Op OP, class G, bool LIVE>
 G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
                       FragSet<G>& y) {
-  region<OP, G, 3, 1, 2, 1>(P, s + 2, acc[0][0], y, at, x);
-  region<OP, G, 1, 1, 3, 1>(P, s + 2, acc[0][1], x, at, ab);
-  region<OP, G, 0, 0, 1, 1>(P, s + 2, acc[1][1], x, ab, at);
-  region<OP, G, 2, 0, 0, 0>(P, s + 3, acc[1][0], y, ab, x);
+  region<OP, G, 3, 1, 2, 1, LIVE>(P, s + 2, acc[0][0], y, at, x);
+  region<OP, G, 1, 1, 3, 1, LIVE>(P, s + 2, acc[0][1], x, at, ab);
+  region<OP, G, 0, 0, 1, 1, LIVE>(P, s + 2, acc[1][1], x, ab, at);
+  region<OP, G, 2, 0, 0, 0, LIVE>(P, s + 3, acc[1][0], y, ab, x);
 }
 
 // Accumulates stages [s0, s1) of tile (tm, tn) into acc.  Leaves every DMA
@@ -646,18 +658,24 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   // The accumulators were just written by VALU (zeroing or a partial tile):
   // wait states before the first MFMA reads them.
   mfma_drain();
-  // Two stages per iteration (the B registers swap roles between them), then
-  // a peeled even stage when the count is odd.
+  // Two stages per iteration (the B registers swap roles between them): pairs
+  // whose DMAs (stages s+2 .. s+4) all exist run without liveness checks, the
+  // last one or two pairs with them, then a peeled even stage when the count
+  // is odd.
   if (stamp) timing_stamp(1);
   int s = s0;
-  const int pairs = (s1 - s0) >> 1;
-  for (int it = 0; it < pairs; ++it, s += 2) {
-    stage_even(P, s, acc, at, ab, x, y);
-    stage_odd(P, s + 1, acc, at, ab, x, y);
+  for (; s + 4 < s1; s += 2) {
+    stage_even<OP, G, true>(P, s, acc, at, ab, x, y);
+    stage_odd<OP, G, true>(P, s + 1, acc, at, ab, x, y);
   }
   settle_acc<G>(acc);
-  if ((s1 - s0) & 1) {
-    stage_even(P, s, acc, at, ab, x, y);
+  for (; s + 1 < s1; s += 2) {
+    stage_even<OP, G, false>(P, s, acc, at, ab, x, y);
+    stage_odd<OP, G, false>(P, s + 1, acc, at, ab, x, y);
+  }
+  settle_acc<G>(acc);
+  if (s < s1) {
+    stage_even<OP, G, false>(P, s, acc, at, ab, x, y);
     settle_acc<G>(acc);
   }
   waitcnt<0, 0>();
