@@ -98,10 +98,22 @@ struct GemmParams {
 constexpr int kTile = 256;
 constexpr int kRowBytes = 128;              // bytes of one operand row per stage
 constexpr int kSubBytes = 128 * kRowBytes;  // one sub-buffer (16 KiB)
-constexpr int kScaleBase = 131072;          // FP4 scale sub-buffers (8 x 1 KiB)
 constexpr int kStageRow = 528;              // epilogue staging row pitch (bytes)
-constexpr int kLdsBytes = 139264;           // 128 KiB operands + 8 KiB scales
-static_assert(kTile * kStageRow <= kLdsBytes, "staging must fit");
+// FP4 E8M0 scales are staged in chunks of kScChunk stages: one chunk holds
+// kScChunk * 8 bytes of each of the tile's 256 A rows and 256 B rows (chunk
+// rows 0-255 = A, 256-511 = B), and two chunk slots sit after the operand
+// buffers.  A chunk row's 32 bytes are two 16-byte halves (stages 0-1, 2-3);
+// rows with bit 3 set store them swapped, so the 16 rows one ds_read_b64
+// serves fall on distinct banks.
+constexpr int kScaleBase = 131072;
+constexpr int kScChunk = 4;
+constexpr int kScRowBytes = 8 * kScChunk;
+constexpr int kScSlotBytes = 512 * kScRowBytes;  // 16 KiB
+// LDS per workgroup: 128 KiB of operand buffers (+ 32 KiB of scale chunks for
+// FP4); the epilogue's staging (256 rows x 528 bytes) reuses it.
+template <bool SCALED>
+constexpr int kLdsBytes = SCALED ? kScaleBase + 2 * kScSlotBytes : kTile * kStageRow;
+static_assert(kTile * kStageRow >= kScaleBase && kTile * kStageRow <= kLdsBytes<true>, "staging must fit");
 
 // Wave geometry: NW waves as WM x WN; per quadrant a wave owns FM x FN MFMA
 // fragments of MD x MD outputs (FM*MD rows of A, FN*MD rows of B).  A
@@ -120,11 +132,10 @@ struct Geo {
   static constexpr int NB = MD * MD / 256;  // 4-float accumulator quads per fragment
   static constexpr int kDmaRows = 128 / NW;        // rows of each sub-buffer one wave loads
   static constexpr int kDmaPerSub = kDmaRows / 8;  // 16-byte DMAs per wave per sub-buffer
-  // FP4 scale DMA: one dword per lane, kDmaRows rows of 8 bytes per wave, so
-  // 2*kDmaRows lanes are active (all 64 for 4 waves, 32 for 8 waves; a
-  // sub-dword LDS-DMA still writes each lane at a 4-byte stride, so it cannot
-  // pack the 8-wave share into fewer bytes per lane).
-  static constexpr int kScaleLanes = 2 * kDmaRows;
+  // FP4 scale chunks: each wave loads 512 / NW chunk rows as kScParts
+  // 16-byte DMAs of 32 rows x 32 bytes.
+  static constexpr int kScRows = 512 / NW;
+  static constexpr int kScParts = kScRows / 32;
   static constexpr int kWavesPerSimd = NW / 4;
   // Row chunk held as the lane's chunk r by lane group gi.  The same map is
   // used for A and B, so it only permutes K inside a stage.
@@ -181,11 +192,40 @@ struct OpInfo {
 template <Op OP>
 constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : G9_MD_F16;
 
+// Per-region work and the DMA pattern of the main loop.  The loop body covers
+// kBody stages = 4 * kBody regions, numbered by their body position.  Every
+// region issues kDmaPerSub operand DMAs per wave.  FP4 adds the scale-chunk
+// DMAs: with a body of two chunks (8 stages), a chunk's kScParts parts are
+// issued at positions 16h + 14 (part 0 of the chunk two ahead of chunk h) and
+// 16h + 0, 2, 4 (the remaining parts of the chunk one ahead), each at least
+// 10 regions before the chunk is first read (position 16h + 14 reads the next
+// chunk's first stage) and after the slot's previous chunk was last read
+// (position 16h + 13).  A region waits for the DMAs issued 7 regions earlier:
+// vmcnt(number of DMAs issued in the 6 regions between), a constant per body
+// position because the pattern repeats every 16 regions.
 template <Op OP, class G>
 struct Shape {
   static constexpr int KS = G::NC / OpInfo<OP>::kChunksPerMfma;  // MFMA steps per stage
   static constexpr int NM = G::FM * G::FN * KS;                  // MFMAs per wave per region
-  static constexpr int kDmaPerRegion = G::kDmaPerSub + (OpInfo<OP>::kScaled ? 1 : 0);
+  static constexpr bool kScaled = OpInfo<OP>::kScaled;
+  static constexpr int kBody = kScaled ? 2 * kScChunk : 2;       // stages per loop iteration
+  static constexpr int kRegions = 4 * kBody;
+  static constexpr int D = G::kDmaPerSub;
+  // Scale-chunk part issued at body position `pos`, or -1.
+  static constexpr int sc_part(int pos) {
+    if (!kScaled) return -1;
+    const int q = pos % 16;
+    if (q == 14) return 0;
+    if (q % 2 == 0 && q / 2 + 1 < G::kScParts) return q / 2 + 1;
+    return -1;
+  }
+  static constexpr int dmas(int pos) { return D + (sc_part(pos) >= 0 ? 1 : 0); }
+  static constexpr int vm_wait(int pos) {
+    int n = 0;
+    for (int q = 1; q <= 6; ++q) n += dmas(((pos - q) % kRegions + kRegions) % kRegions);
+    return n;
+  }
+  static_assert(vm_wait(0) < 64, "vmcnt is 6 bits");
 };
 
 template <class G>
@@ -217,7 +257,6 @@ G9_DEV V load_quads(const f32x4* p) {
 
 // LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
 constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s) * kSubBytes; }
-constexpr int scale_off(int X, int s) { return kScaleBase + (X * 2 + s) * 1024; }
 
 // Block-scaled MFMA step E: byte E of each scale VGPR is the scale
 // (op_sel and op_sel_hi bit 0 of the scale operands select the byte).
@@ -323,7 +362,7 @@ struct Slots {
   static constexpr int scale_q(int F) { return 1 + F * kScaleStep; }
   static constexpr int D = G::kDmaPerSub;
   static constexpr int dma_q(int J) { return NQ == 1 ? 0 : 1 + J * (NQ - 1) / D; }
-  static constexpr int kScaleDmaQ = NQ > 5 ? 5 : NQ - 1;
+  static constexpr int kScaleDmaQ = dma_q(D - 1) + 2 < NQ ? dma_q(D - 1) + 2 : NQ - 1;
   static constexpr int kLastQ = (read_q(NR - 1) > scale_q(NF - 1) ? read_q(NR - 1) : scale_q(NF - 1)) + 3;
   static constexpr int kPermQ = (kLastQ > NQ - 8 ? kLastQ : NQ - 8) < NQ - 1 ? (kLastQ > NQ - 8 ? kLastQ : NQ - 8)
                                                                               : NQ - 1;
@@ -344,52 +383,59 @@ G9_DEV u32 opaque_s(u32 x) {
   return x;
 }
 
+// SGPR offset of a DMA for a stage past the end of K: the buffer range check
+// covers voffset + soffset + imm, every resource holds at most 2^31 bytes
+// (128 rows x a row stride of at most 2^24) and voffset + imm stays below
+// 2^31, so the access is out of range (it reads zeros, without memory
+// traffic) and the sum does not wrap.
+constexpr u32 kDeadOff = 0x80000000u;
+
 // Per-workgroup pipeline state: buffer resources, per-lane DMA offsets and LDS
 // read bases.  One instance per output tile (rebuilt per stream-K segment).
 template <Op OP, class G>
 struct Pipe {
   using I = OpInfo<OP>;
   static constexpr int D = G::kDmaPerSub;
-  rsrc_t rA[2], rB[2], rZ;  // operand half-tiles; rZ has no valid bytes (reads 0)
-  rsrc_t rSA[2], rSB[2];    // FP4 scale half-tiles
+  static constexpr int SP = I::kScaled ? G::kScParts : 1;
+  rsrc_t rA[2], rB[2];      // operand half-tiles
+  rsrc_t rS;                // FP4: the scale rows this wave loads into the chunks
   u32 vA[D], vB[D];         // DMA offsets of the wave's 1-KiB runs
-  u32 vSA, vSB;             // FP4 scale DMA offsets
+  u32 vS[SP];               // FP4: chunk DMA offsets (32 rows x 32 bytes each)
   u32 bA[G::NC], bB[G::NC];  // LDS read bases of the lane's chunks (A at 0, B at 64 KiB)
-  u32 bSA, bSB;             // FP4 LDS read bases of the lane's scale row (at 128 KiB)
+  u32 bS[2][2];             // FP4: LDS read bases [A/B][stages 0-1 / 2-3 of a chunk]
   u32 sel;                  // FP4, MD 16: scale byte selector
   u32 lds0;                 // LDS address of the shared buffer
   u32 mrow;                 // LDS address of the wave's rows in sub-buffer A0, slot 0
-  u32 msc;                  // LDS address of the wave's rows in scale sub-buffer A0, slot 0
+  u32 msc;                  // FP4: LDS address of the wave's chunk rows in chunk slot 0
   int wave;
+  int s0;                   // first stage of the range (chunks are counted from here)
   int s_end;                // first stage not to load
 
-  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int end) {
+  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int first, int end) {
     // Tile coordinates are wave-uniform; saying so keeps the buffer resources
     // in SGPRs (a resource the compiler thinks divergent is issued through a
     // per-lane "waterfall" loop around every DMA).
     tm = __builtin_amdgcn_readfirstlane(tm);
     tn = __builtin_amdgcn_readfirstlane(tn);
+    s0 = __builtin_amdgcn_readfirstlane(first);
     s_end = __builtin_amdgcn_readfirstlane(end);
     lds0 = (u32)(uintptr_t)to_lds(smem);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     mrow = lds0 + (u32)wave * (G::kDmaRows * kRowBytes);
-    msc = lds0 + kScaleBase + (u32)wave * (G::kDmaRows * 8);
     const int wm = wave / G::WN, wn = wave % G::WN;
     const int gi = lane / G::MD, rr = lane % G::MD;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int ra = tm * kTile + h * 128, rb = tn * kTile + h * 128;
-      const int va = min(max(p.M - ra, 0), 128), vb = min(max(p.N - rb, 0), 128);
+      // Valid rows (the clamp is a VALU med3): stated uniform, so the
+      // resources stay in SGPRs.
+      const int va = __builtin_amdgcn_readfirstlane(min(max(p.M - ra, 0), 128));
+      const int vb = __builtin_amdgcn_readfirstlane(min(max(p.N - rb, 0), 128));
       rA[h] = make_rsrc(p.a + (size_t)ra * p.lda, (u32)va * p.lda);
       rB[h] = make_rsrc(p.b + (size_t)rb * p.ldb, (u32)vb * p.ldb);
-      if constexpr (I::kScaled) {
-        rSA[h] = make_rsrc(p.a_sc + (size_t)ra * p.ldsa, (u32)va * p.ldsa);
-        rSB[h] = make_rsrc(p.b_sc + (size_t)rb * p.ldsb, (u32)vb * p.ldsb);
-      }
     }
-    rZ = make_rsrc(p.a, 0);
     // DMA j of a sub-buffer covers rows 8j..8j+7 of the wave's share and is
     // issued with immediate offset 1024j, which advances the LDS destination
     // by 1024j as well, so the four DMAs of a region share one M0.  The global
@@ -413,24 +459,51 @@ struct Pipe {
       bB[c] = opaque(lds0 + 65536u + (u32)(wn * G::FN * G::MD + rr) * kRowBytes + slot * 16);
     }
     if constexpr (I::kScaled) {
-      // Each wave loads kDmaRows scale rows of 8 bytes, two dwords per row.
-      const int row = G::kDmaRows * wave + (lane >> 1);
-      vSA = (u32)row * p.ldsa + (lane & 1) * 4;
-      vSB = (u32)row * p.ldsb + (lane & 1) * 4;
-      // MD 16 reads the row's 8 scale bytes and picks groups gi and 4 + gi
-      // (byte 0x0c of a v_perm selector yields zero); MD 32 reads the dword
-      // of groups 4gi..4gi+3 directly.
+      // The wave loads chunk rows [xw * 128 + r0, + kScRows) of the 512: half
+      // tile xw (0: A0, 1: A1, 2: B0, 3: B1), rows r0.. of it.  Part j covers
+      // 32 of them, two lanes per row; lane l fetches the 16-byte half that
+      // belongs in its LDS half under the bit-3 row swap.
+      // The resource is built from wave-uniform scalars (a select between
+      // prebuilt resources is lowered through VGPRs, which turns every DMA
+      // into a per-lane loop).
+      const int xw = wave / (G::NW / 4);
+      const int r0 = (wave % (G::NW / 4)) * G::kScRows;
+      const bool sa = xw < 2;
+      const u32 lds = sa ? p.ldsa : p.ldsb;
+      const int hrow = (sa ? tm : tn) * kTile + (xw & 1) * 128;
+      const int hvalid = __builtin_amdgcn_readfirstlane(min(max((sa ? p.M : p.N) - hrow, 0), 128));
+      const unsigned char* hbase = (sa ? p.a_sc : p.b_sc) + (size_t)hrow * lds;
+      rS = make_rsrc(hbase, (u32)hvalid * lds);
+#pragma unroll
+      for (int j = 0; j < SP; ++j) {
+        const int row = r0 + 32 * j + (lane >> 1);
+        const int half = (lane & 1) ^ ((row >> 3) & 1);
+        vS[j] = (u32)row * lds + half * 16;
+      }
+      msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
+      // MD 16 reads the row's 8 scale bytes of a stage and picks groups gi
+      // and 4 + gi (byte 0x0c of a v_perm selector yields zero); MD 32 reads
+      // the dword of groups 4gi..4gi+3 directly.  Fragment rows are multiples
+      // of 16, so the row swap depends on rr only.
       const u32 word = G::MD == 32 ? 4u * gi : 0u;
-      bSA = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * 8 + word);
-      bSB = opaque(lds0 + kScaleBase + (u32)(wn * G::FN * G::MD + rr) * 8 + word);
+      const int ssw = (rr >> 3) & 1;
+#pragma unroll
+      for (int g = 0; g < (G::NW == 4 ? 2 : 1); ++g) {
+        bS[0][g] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
+        bS[1][g] =
+            opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
+      }
       sel = (u32)gi | ((u32)(4 + gi) << 8) | 0x0c0c0000u;
     } else {
       sel = 0;
     }
   }
 
-  G9_DEV rsrc_t src(int X, bool live) const { return live ? (X < 2 ? rA[X & 1] : rB[X & 1]) : rZ; }
-  G9_DEV rsrc_t src_sc(int X, bool live) const { return live ? (X < 2 ? rSA[X & 1] : rSB[X & 1]) : rZ; }
+  G9_DEV rsrc_t src(int X) const { return X < 2 ? rA[X & 1] : rB[X & 1]; }
+  // SGPR offset of stage `stage` in an operand row (kDeadOff past the end).
+  G9_DEV u32 stage_off(int stage) const { return stage < s_end ? (u32)stage * kRowBytes : kDeadOff; }
+  // SGPR offset of the chunk starting at stage `stage` in a scale row.
+  G9_DEV u32 chunk_off(int stage) const { return stage < s_end ? (u32)stage * 8 : kDeadOff; }
 
   // 16-byte DMA number J (rows 8J..8J+7 of the wave's kDmaRows) of sub-buffer X.
   // `mb` is mrow, passed through opaque_s once per region: the 8 distinct
@@ -442,16 +515,11 @@ struct Pipe {
     const u32 dst = mb + sub_off(X, SLOT);
     dma16<J * 1024>(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vA[J] : vB[J], soff);
   }
-  template <int X, int SLOT>
-  G9_DEV void dma_scales(rsrc_t r, u32 soff, u32 mb) const {
-    const u32 dst = mb + (scale_off(X, SLOT) - kScaleBase);
-    if constexpr (G::kScaleLanes == 64) {
-      dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
-    } else {
-      // Lanes beyond the wave's rows are masked off; the instruction is still
-      // issued by every wave, so vmcnt counts stay uniform.
-      if ((threadIdx.x & 63) < G::kScaleLanes) dma4(r, (G9_LDS void*)(uintptr_t)dst, X < 2 ? vSA : vSB, soff);
-    }
+  // Part J of the scale chunk whose rows start at `soff` bytes, into chunk slot SSLOT.
+  template <int SSLOT, int J>
+  G9_DEV void dma_chunk(u32 soff, u32 mb) const {
+    const u32 dst = mb + SSLOT * kScSlotBytes + J * 1024;
+    dma16(rS, (G9_LDS void*)(uintptr_t)dst, vS[J], soff);
   }
 
   // 16-byte LDS read number R (fragment R / NC, chunk R % NC) of sub-buffer X.
@@ -463,10 +531,19 @@ struct Pipe {
     const u32 base = X < 2 ? bA[R % NC] : bB[R % NC];
     f[R / NC].c[R % NC] = *(const G9_LDS u32x4*)(uintptr_t)(base + imm);
   }
-  template <int X, int SLOT, int F>
+  // Scales of fragment F of sub-buffer X for stage ST of the chunk in slot SSLOT.
+  template <int X, int SSLOT, int ST, int F>
   G9_DEV void read_scales(FragSet<G>& f) const {
-    constexpr int imm = scale_off(X, SLOT) - kScaleBase + F * G::MD * 8;
-    const u32 base = X < 2 ? bSA : bSB;
+    constexpr int imm = SSLOT * kScSlotBytes + (X & 1) * 128 * kScRowBytes + F * G::MD * kScRowBytes + 8 * (ST & 1);
+    u32 base = bS[X >= 2][0];
+    if constexpr (G::NW == 4) {
+      base = bS[X >= 2][ST >> 1];
+    } else if constexpr (ST >= 2) {
+      // 8 waves have half the VGPRs: the stages 2-3 base differs from the
+      // stages 0-1 base in address bit 4 only (the half swap), so it is formed
+      // at the read (inline, so it is not hoisted into a loop-long register).
+      asm volatile("v_xor_b32 %0, 16, %0" : "+v"(base));
+    }
     if constexpr (G::MD == 16)
       f[F].sc = *(const G9_LDS u32x2*)(uintptr_t)(base + imm);
     else
@@ -476,20 +553,22 @@ struct Pipe {
   // Whole-set variants for the prologue.
   template <int X, int SLOT>
   G9_DEV void issue(int stage) const {
-    const bool live = stage < s_end;
-    const rsrc_t r = src(X, live);
-    const u32 soff = (u32)stage * kRowBytes;
+    const rsrc_t r = src(X);
+    const u32 soff = stage_off(stage);
     [&]<int... J>(std::integer_sequence<int, J...>) { (dma_rows<X, SLOT, J>(r, soff, mrow), ...); }(
         std::make_integer_sequence<int, D>{});
-    if constexpr (I::kScaled) dma_scales<X, SLOT>(src_sc(X, live), (u32)stage * 8, msc);
   }
-  template <int X, int SLOT>
+  template <int SSLOT, int J>
+  G9_DEV void issue_chunk(int stage) const {
+    dma_chunk<SSLOT, J>(chunk_off(stage), msc);
+  }
+  template <int X, int SLOT, int SSLOT, int ST>
   G9_DEV void load(FragSet<G>& f) const {
     constexpr int NF = X < 2 ? G::FM : G::FN;
     [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
         std::make_integer_sequence<int, G::NC * NF>{});
     if constexpr (I::kScaled) {
-      [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SLOT, F>(f), ...); }(
+      [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SSLOT, ST, F>(f), ...); }(
           std::make_integer_sequence<int, NF>{});
     }
   }
@@ -533,15 +612,26 @@ G9_DEV void settle_acc(Acc<G>& acc) {
   pin_acc<G>(acc);
 }
 
-// Slot K of a region: MFMA number K (step-major: step, A fragment, B
-// fragment), then whatever the slot table puts after it, then a hard
-// scheduling fence (the MFMAs are inline assembly, which the scheduler's
+// Slot K of the region at body position POS: MFMA number K (step-major: step,
+// A fragment, B fragment), then whatever the slot table puts after it, then a
+// hard scheduling fence (the MFMAs are inline assembly, which the scheduler's
 // instruction-class masks do not cover, so only a full fence pins the order).
-template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int K>
-G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32 soff_sc, u32 mb, QAcc<G>& acc,
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS, int K>
+G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u32 mb, u32 ms, QAcc<G>& acc,
                         const FragSet<G>& bx, const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
+  using Sh = Shape<OP, G>;
+  // The stage (in the body) whose operands this region reads: the current one
+  // in regions 0-1, the next one in regions 2-3; its scale chunk slot and
+  // stage within the chunk.
+  constexpr int ks = POS / 4 + (POS % 4 >= 2 ? 1 : 0);
+  constexpr int kSSlot = (ks / kScChunk) % 2, kSt = ks % kScChunk;
+  // Scale-chunk DMA of this position: part 0 goes to the chunk two ahead of
+  // the current one (the current chunk's slot, free since position 16h + 13),
+  // the other parts to the next chunk's slot.
+  constexpr int part = Sh::sc_part(POS);
+  constexpr int kDSSlot = part == 0 ? (POS / 16) % 2 : (POS / 16 + 1) % 2;
   constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j = K % G::FN;
   mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
   constexpr int q = K - S::kPre;
@@ -551,13 +641,14 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32
     });
     if constexpr (OpInfo<OP>::kScaled) {
       static_for<NF>([&](auto F) {
-        if constexpr (S::scale_q(decltype(F)::value) == q) P.template read_scales<RX, RSLOT, decltype(F)::value>(nxt);
+        if constexpr (S::scale_q(decltype(F)::value) == q)
+          P.template read_scales<RX, kSSlot, kSt, decltype(F)::value>(nxt);
       });
     }
     static_for<S::D>([&](auto J) {
       if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
     });
-    if constexpr (OpInfo<OP>::kScaled && q == S::kScaleDmaQ) P.template dma_scales<DX, DSLOT>(rs, soff_sc, opaque_s(P.msc));
+    if constexpr (part >= 0 && q == S::kScaleDmaQ) P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, ms);
     if constexpr (OpInfo<OP>::kScaled && G::MD == 16 && q == S::kPermQ) {
       waitcnt<63, 0>();
       P.template gather_scales<RX>(nxt);
@@ -566,62 +657,73 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, rsrc_t rs, u32 soff, u32
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// One quadrant region: MFMAs of (bx, ay) into acc, LDS reads of sub-buffer
-// RX/RSLOT into nxt, DMA of stage `ds` into sub-buffer DX/DSLOT.
-//   s_waitcnt vmcnt(6 groups) lgkmcnt(0)   -- DMA of the set read now landed,
+// The quadrant region at body position POS (region POS % 4 of stage s + POS / 4,
+// with s the body's first stage): MFMAs of (bx, ay) into acc, LDS reads of
+// sub-buffer RX/RSLOT into nxt, DMA of stage `ds` into sub-buffer DX/DSLOT.
+//   s_waitcnt vmcnt(DMAs of the 6 previous regions) lgkmcnt(0)
+//                                          -- DMA of the set read now landed,
 //                                             the previous region's reads done
 //   kPre MFMAs
 //   s_barrier                              -- every wave's DMA landed and every
 //                                             wave done reading the sub-buffer
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
-//
-// LIVE: the caller guarantees stage `ds` exists, so the operand resources are
-// used directly; otherwise a stage past the end reads from the empty resource
-// (zeros, no memory traffic) and the per-region choice costs a few SALU
-// selects, which the main loop avoids by running LIVE until its last pairs.
-template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, bool LIVE>
-G9_DEV void region(const Pipe<OP, G>& P, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS>
+G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
                    FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
+  using Sh = Shape<OP, G>;
   __builtin_amdgcn_sched_barrier(0);
-  waitcnt<6 * Shape<OP, G>::kDmaPerRegion, 0>();
-  const bool live = LIVE || ds < P.s_end;
-  const rsrc_t r = P.src(DX, live);
-  rsrc_t rs = r;
-  if constexpr (OpInfo<OP>::kScaled) rs = P.src_sc(DX, live);
-  const u32 soff = (u32)ds * kRowBytes, soff_sc = (u32)ds * 8;
+  waitcnt<Sh::vm_wait(POS), 0>();
+  const rsrc_t r = P.src(DX);
+  const u32 soff = P.stage_off(ds);
   const u32 mb = opaque_s(P.mrow);
+  u32 soff_sc = 0, ms = 0;
+  if constexpr (Sh::sc_part(POS) >= 0) {
+    soff_sc = P.chunk_off(s + kScChunk * (POS / 16) + (Sh::sc_part(POS) == 0 ? 2 : 1) * kScChunk);
+    ms = opaque_s(P.msc);
+  }
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K>(P, r, rs, soff, soff_sc, mb, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K>(P, r, soff, soff_sc, mb, ms, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::kPre>{});
   barrier();
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, K + S::kPre>(P, r, rs, soff, soff_sc, mb, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K + S::kPre>(P, r, soff, soff_sc, mb, ms, acc, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
-// Even stage (slot 0): B0 fragments in x; B1 fragments go to y, and after
-// they are consumed the next stage's B0 fragments go to y as well.
-template <Op OP, class G, bool LIVE>
-G9_DEV void stage_even(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
-                       FragSet<G>& y) {
-  region<OP, G, 3, 0, 2, 0, LIVE>(P, s + 2, acc[0][0], x, at, y);
-  region<OP, G, 1, 0, 3, 0, LIVE>(P, s + 2, acc[0][1], y, at, ab);
-  region<OP, G, 0, 1, 1, 0, LIVE>(P, s + 2, acc[1][1], y, ab, at);
-  region<OP, G, 2, 1, 0, 1, LIVE>(P, s + 3, acc[1][0], x, ab, y);
+// Stage K of the body starting at stage s.  Even stages (operand slot 0): B0
+// fragments in x; B1 fragments go to y, and after they are consumed the next
+// stage's B0 fragments go to y as well.  Odd stages (slot 1): B0 in y; B1 to
+// x, then the next stage's B0.
+template <Op OP, class G, int K>
+G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
+                  FragSet<G>& y) {
+  constexpr int POS = 4 * K;
+  if constexpr (K % 2 == 0) {
+    region<OP, G, 3, 0, 2, 0, POS + 0>(P, s, s + K + 2, acc[0][0], x, at, y);
+    region<OP, G, 1, 0, 3, 0, POS + 1>(P, s, s + K + 2, acc[0][1], y, at, ab);
+    region<OP, G, 0, 1, 1, 0, POS + 2>(P, s, s + K + 2, acc[1][1], y, ab, at);
+    region<OP, G, 2, 1, 0, 1, POS + 3>(P, s, s + K + 3, acc[1][0], x, ab, y);
+  } else {
+    region<OP, G, 3, 1, 2, 1, POS + 0>(P, s, s + K + 2, acc[0][0], y, at, x);
+    region<OP, G, 1, 1, 3, 1, POS + 1>(P, s, s + K + 2, acc[0][1], x, at, ab);
+    region<OP, G, 0, 0, 1, 1, POS + 2>(P, s, s + K + 2, acc[1][1], x, ab, at);
+    region<OP, G, 2, 0, 0, 0, POS + 3>(P, s, s + K + 3, acc[1][0], y, ab, x);
+  }
 }
 
-// Odd stage (slot 1): B0 fragments in y; B1 fragments go to x, then the next
-// stage's B0 fragments.
-template <Op OP, class G, bool LIVE>
-G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
-                      FragSet<G>& y) {
-  region<OP, G, 3, 1, 2, 1, LIVE>(P, s + 2, acc[0][0], y, at, x);
-  region<OP, G, 1, 1, 3, 1, LIVE>(P, s + 2, acc[0][1], x, at, ab);
-  region<OP, G, 0, 0, 1, 1, LIVE>(P, s + 2, acc[1][1], x, ab, at);
-  region<OP, G, 2, 0, 0, 0, LIVE>(P, s + 3, acc[1][0], y, ab, x);
+// The last n < kBody stages (a partial body): stages 0 .. n-1.
+template <Op OP, class G, int K>
+G9_DEV void tail(const Pipe<OP, G>& P, int s, int n, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
+                 FragSet<G>& y) {
+  if constexpr (K + 1 < Shape<OP, G>::kBody) {
+    if (n > K) {
+      stage<OP, G, K>(P, s, acc, at, ab, x, y);
+      tail<OP, G, K + 1>(P, s, n, acc, at, ab, x, y);
+    }
+  }
 }
 
 // Accumulates stages [s0, s1) of tile (tm, tn) into acc.  Leaves every DMA
@@ -629,10 +731,15 @@ G9_DEV void stage_odd(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, 
 template <Op OP, class G>
 G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, Acc<G>& acc,
                      bool stamp = false) {
-  constexpr int DQ = Shape<OP, G>::kDmaPerRegion;
+  using Sh = Shape<OP, G>;
+  constexpr bool kScaled = OpInfo<OP>::kScaled;
   Pipe<OP, G> P;
-  P.init(p, smem, tm, tn, s1);
-  // DMA stream order: per stage A0, B0, B1, A1.  Stage s lives in slot (s-s0)&1.
+  P.init(p, smem, tm, tn, s0, s1);
+  // Scale chunk 0 (stages s0 .. s0+3) first, then the operands in DMA stream
+  // order, per stage A0, B0, B1, A1 (stage s lives in slot (s-s0)&1), with
+  // part 0 of chunk 1 where body position 30 would issue it: the prologue
+  // then leaves the DMA counts the first body's waits expect.
+  if constexpr (kScaled) static_for<G::kScParts>([&](auto J) { P.template issue_chunk<0, decltype(J)::value>(s0); });
   P.template issue<0, 0>(s0);
   P.template issue<2, 0>(s0);
   P.template issue<3, 0>(s0);
@@ -641,15 +748,17 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   P.template issue<2, 1>(s0 + 1);
   P.template issue<3, 1>(s0 + 1);
   P.template issue<1, 1>(s0 + 1);
-  // A0(s0) and B0(s0) landed: read them, then (once every wave has) refill
-  // A0 slot 0 with stage s0+2.
-  waitcnt<6 * DQ, 0>();
+  if constexpr (kScaled) P.template issue_chunk<1, 0>(s0 + kScChunk);
+  // A0(s0) and B0(s0) landed (and chunk 0, issued before them): read them,
+  // then (once every wave has) refill A0 slot 0 with stage s0+2.
+  constexpr int kFirst = 6 * Sh::D + (kScaled ? 1 : 0);
+  waitcnt<kFirst, 0>();
   barrier();
   FragSet<G> at, ab, x, y;
-  P.template load<0, 0>(at);
-  P.template load<2, 0>(x);
-  waitcnt<6 * DQ, 0>();
-  if constexpr (OpInfo<OP>::kScaled && G::MD == 16) {
+  P.template load<0, 0, 0, 0>(at);
+  P.template load<2, 0, 0, 0>(x);
+  waitcnt<kFirst, 0>();
+  if constexpr (kScaled && G::MD == 16) {
     P.template gather_scales<0>(at);
     P.template gather_scales<2>(x);
   }
@@ -658,24 +767,15 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   // The accumulators were just written by VALU (zeroing or a partial tile):
   // wait states before the first MFMA reads them.
   mfma_drain();
-  // Two stages per iteration (the B registers swap roles between them): pairs
-  // whose DMAs (stages s+2 .. s+4) all exist run without liveness checks, the
-  // last one or two pairs with them, then a peeled even stage when the count
-  // is odd.
+  // kBody stages per iteration (the B registers swap roles between stages),
+  // then the remaining stages as a partial body.
   if (stamp) timing_stamp(1);
   int s = s0;
-  for (; s + 4 < s1; s += 2) {
-    stage_even<OP, G, true>(P, s, acc, at, ab, x, y);
-    stage_odd<OP, G, true>(P, s + 1, acc, at, ab, x, y);
-  }
-  settle_acc<G>(acc);
-  for (; s + 1 < s1; s += 2) {
-    stage_even<OP, G, false>(P, s, acc, at, ab, x, y);
-    stage_odd<OP, G, false>(P, s + 1, acc, at, ab, x, y);
-  }
+  for (; s + Sh::kBody <= s1; s += Sh::kBody)
+    static_for<Sh::kBody>([&](auto K) { stage<OP, G, decltype(K)::value>(P, s, acc, at, ab, x, y); });
   settle_acc<G>(acc);
   if (s < s1) {
-    stage_even<OP, G, false>(P, s, acc, at, ab, x, y);
+    tail<OP, G, 0>(P, s, s1 - s, acc, at, ab, x, y);
     settle_acc<G>(acc);
   }
   waitcnt<0, 0>();
@@ -756,7 +856,7 @@ G9_DEV float epilogue_scale(const GemmParams& p) {
 // Data-parallel schedule: one workgroup per 256x256 output tile.
 template <Op OP, int OUT, class G>
 G9_DEV void gemm_dp(const GemmParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes<OpInfo<OP>::kScaled>];
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, tm, tn);
   Acc<G> acc;
@@ -851,7 +951,7 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
 
 template <Op OP, int OUT, class G>
 G9_DEV void gemm_sk(const GemmParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes<OpInfo<OP>::kScaled>];
   const int G_ = p.sk_ctas;
   // Workgroup ids are dispatched round-robin over the XCDs; give each XCD a
   // contiguous run of ranges so chained neighbours share an L2.
