@@ -18,7 +18,7 @@ using namespace g9;
 
 #define G9_DEFINE(NAME, OP, OUT)                                                                    \
   using NAME##_g4 = Geo4<kMfmaDim<OP>>;                                                             \
-  using NAME##_g8 = Geo8<kMfmaDim<OP>>;                                                             \
+  using NAME##_g8 = Geo8<kMfmaDim8<OP>>;                                                            \
   extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_dp_4w(GemmParams p) {                       \
     gemm_dp<OP, OUT, NAME##_g4>(p);                                                                 \
   }                                                                                                 \

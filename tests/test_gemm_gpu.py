@@ -289,7 +289,10 @@ def test_launch_on_side_stream_and_preallocated_c(gpu):
 
 # ---------------------------------------------------------------------------
 # 8-wave (inter_wave) kernels: same per-element MFMA sequence as the 4-wave
-# kernels, so their outputs must be bitwise equal.
+# kernels for FP16/BF16/BF8, so their outputs must be bitwise equal.  The
+# 8-wave MXFP4 kernel uses 32x32x64 MFMAs (4-wave: 16x16x128): the same exact
+# products, summed in another order inside the MFMA, so it matches the exact
+# fixtures bit for bit and the 4-wave kernel to fp32 rounding.
 # ---------------------------------------------------------------------------
 from gfx950_gluon_tutorials_amd.gemm.inter_wave import a4w4 as iw_a4w4  # noqa: E402
 from gfx950_gluon_tutorials_amd.gemm.inter_wave import a8w8 as iw_a8w8  # noqa: E402
@@ -326,8 +329,8 @@ def test_inter_wave_exact_fixtures(gpu, schedule):
 
 
 @pytest.mark.parametrize("kind", ["fp16", "bf16", "bf8", "mxfp4"])
-def test_8wave_bitwise_equals_4wave_at_baseline_size(gpu, kind):
-    _say(f"8-wave == 4-wave {kind} 4096x4096x8192")
+def test_8wave_matches_4wave_at_baseline_size(gpu, kind):
+    _say(f"8-wave vs 4-wave {kind} 4096x4096x8192")
     gen = torch.Generator().manual_seed({"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3}[kind])
     x = _randn(gen, (4096, 8192))
     y = _randn(gen, (4096, 8192))
@@ -353,5 +356,10 @@ def test_8wave_bitwise_equals_4wave_at_baseline_size(gpu, kind):
     c8sk = run(8, "streamk")
     torch.cuda.synchronize()
     _check_streamk_clean(gpu)
-    np.testing.assert_array_equal(_bits(c8), _bits(c4))
-    np.testing.assert_array_equal(_bits(c8sk), _bits(c4))
+    if kind == "mxfp4":
+        # bf16 outputs of fp32 sums that differ in the last bits: a few
+        # elements land one bf16 step apart.
+        assert R.rel_frobenius(_f32(c8), _f32(c4)) < 2e-4
+    else:
+        np.testing.assert_array_equal(_bits(c8), _bits(c4))
+    np.testing.assert_array_equal(_bits(c8sk), _bits(c8))
