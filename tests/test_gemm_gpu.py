@@ -206,6 +206,53 @@ def test_a4w4_baseline_config(gpu):
     assert err <= 1e-3, f"relative Frobenius error {err:.3g}"
 
 
+# Stage counts around the loop structure: the MXFP4 loop body is 8 stages (two
+# 4-stage scale chunks), the others 2; shorter counts run only the tail, and
+# the last stages' DMAs fall past the end of K.  Ragged M/N add edge tiles.
+# Stream-K splits these into segments that start at any stage.
+@pytest.mark.parametrize("ns", [1, 2, 3, 4, 5, 7, 8, 9, 10, 17])
+@pytest.mark.parametrize("waves", [4, 8])
+def test_a4w4_stage_counts(gpu, ns, waves):
+    M, N, K = 300, 264, 256 * ns
+    _say(f"a4w4 {M}x{N}x{K} waves={waves}")
+    gen = torch.Generator().manual_seed(100 + ns)
+    pa, sa = quant.quantize_mxfp4(_randn(gen, (M, K)))
+    pb, sb = quant.quantize_mxfp4(_randn(gen, (N, K)))
+    args = [t.to(gpu) for t in (pa, pb, sa, sb)]
+    outs = {}
+    for sched in SCHEDULES:
+        c = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+        outs[sched] = _launch.gemm_a4w4(*args, c, schedule=sched, waves=waves)
+    torch.cuda.synchronize()
+    _check_streamk_clean(gpu)
+    ref = R.a4w4_ref(pa.numpy(), pb.numpy(), sa.numpy(), sb.numpy(), "bf16")
+    err = R.rel_frobenius(_f32(outs["dp"]), ref)
+    assert err <= 1e-3, f"relative Frobenius error {err:.3g}"
+    np.testing.assert_array_equal(_bits(outs["streamk"]), _bits(outs["dp"]))
+
+
+@pytest.mark.parametrize("ns", [1, 2, 3, 5, 9])
+@pytest.mark.parametrize("waves", [4, 8])
+def test_a8w8_stage_counts(gpu, ns, waves):
+    M, N, K = 260, 300, 128 * ns
+    _say(f"a8w8 {M}x{N}x{K} waves={waves}")
+    gen = torch.Generator().manual_seed(200 + ns)
+    qa, sa = quant.quantize_e5m2(_randn(gen, (M, K)))
+    qb, sb = quant.quantize_e5m2(_randn(gen, (N, K)))
+    a, b = qa.to(gpu), qb.to(gpu)
+    outs = {}
+    for sched in SCHEDULES:
+        c = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+        outs[sched] = _launch.gemm_a8w8(a, b.T, c, a_scale=sa.to(gpu), b_scale=sb.to(gpu), schedule=sched,
+                                        waves=waves)
+    torch.cuda.synchronize()
+    _check_streamk_clean(gpu)
+    ref = R.a8w8_ref(qa.view(torch.uint8).numpy(), qb.view(torch.uint8).numpy(), float(sa), float(sb), "bf16")
+    err = R.rel_frobenius(_f32(outs["dp"]), ref)
+    assert err <= 1e-3, f"relative Frobenius error {err:.3g}"
+    np.testing.assert_array_equal(_bits(outs["streamk"]), _bits(outs["dp"]))
+
+
 @pytest.mark.parametrize("M,N,K", [(3840, 3840, 16384), (8192, 1280, 8192)])
 def test_streamk_bit_identical_to_dp(gpu, M, N, K):
     """fp16 randn(seed=4)*0.1; stream-K output == data-parallel output, bit for bit."""
