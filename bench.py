@@ -65,6 +65,8 @@ def parse_args():
     p.add_argument("--serialized", type=int, default=1,
                    help="also time the reference's protocol: serialized dispatches, mean of the last 100 of 1000")
     p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
+    p.add_argument("--telemetry-s", type=float, default=3.0,
+                   help="run the headline case this long while sampling board power and clock (0: skip)")
     p.add_argument("--summarize", default="",
                    help="print a per-kernel summary of the rocprofv3 SQLite output under this directory and exit")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -164,6 +166,72 @@ def time_case(launch, steps, warmup, schedule="dp", settle_s=0.0):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms per launch
+
+
+def _smi_sample(exe: str):
+    """One amd-smi reading: (socket power W, mean GFX clock MHz over the XCDs)."""
+    import subprocess
+
+    out = subprocess.run([exe, "metric", "-g", "0", "-p", "-c", "--json"], capture_output=True, text=True,
+                         timeout=10).stdout
+    d = json.loads(out)
+    g = d[0] if isinstance(d, list) else d
+    if isinstance(g, dict) and "gpu_data" in g:
+        g = g["gpu_data"][0]
+    pw = g.get("power", {}).get("socket_power")
+    pw = pw.get("value") if isinstance(pw, dict) else pw
+    clk = [v["clk"]["value"] for k, v in g.get("clock", {}).items()
+           if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+    return (float(pw) if pw not in (None, "N/A") else None), (sum(clk) / len(clk) if clk else None)
+
+
+def telemetry(launch, secs: float):
+    """Runs `launch` back to back for `secs` seconds while a child amd-smi
+    process samples the board power and GFX clock; returns the medians over
+    the second half of the window and the launch time there (None without
+    amd-smi).  Evidence for the power limit: the FP16/BF16 GEMMs hold the
+    board at its 1400 W cap with the clock well below its 2.4 GHz peak."""
+    import shutil
+    import statistics as st
+    import threading
+
+    import torch
+
+    exe = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    if not os.path.exists(exe):
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            try:
+                samples.append((time.perf_counter(), *_smi_sample(exe)))
+            except Exception:  # a failed reading is skipped
+                pass
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    blocks, i = [], 0
+    while time.perf_counter() - t0 < secs:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(50):
+            launch(i)
+            i += 1
+        e1.record()
+        torch.cuda.synchronize()
+        blocks.append((time.perf_counter(), e0.elapsed_time(e1) / 50))
+    stop.set()
+    th.join(timeout=15)
+    half = t0 + secs / 2
+    pw = [p for t, p, c in samples if t >= half and p is not None]
+    ck = [c for t, p, c in samples if t >= half and c is not None]
+    ms = [m for t, m in blocks if t >= half]
+    if not pw or not ck or not ms:
+        return None
+    return {"seconds": secs, "samples": len(pw), "power_w": st.median(pw), "gfx_clock_mhz": round(st.median(ck)),
+            "launch_us": round(st.median(ms) * 1e3, 2), "tool": "amd-smi metric -p -c"}
 
 
 def time_serialized(launch, n=1000, last=100):
@@ -328,6 +396,14 @@ def main():
         if ref:
             msg += f"  | reference {ref:.0f}"
         print(msg, flush=True)
+        if args.telemetry_s > 0 and not args.only and kk == K and w == 4:
+            tel = telemetry(launch, args.telemetry_s)
+            if tel:
+                tel["tflops"] = round(2.0 * M * N * kk / tel["launch_us"] / 1e6, 1)
+                results[key]["telemetry"] = tel
+                print(f"#   steady state {tel['launch_us']:.1f} us ({tel['tflops']:.0f} TFLOPS) at "
+                      f"{tel['power_w']:.0f} W, GFX clock {tel['gfx_clock_mhz']} MHz (amd-smi, {tel['samples']} samples)",
+                      flush=True)
         del launch
         torch.cuda.empty_cache()
     sk = {}

@@ -17,7 +17,14 @@ Per workgroup (all its SIMDs run the same schedule):
   2048 (BF8, K_stage 128) or 4096 (MXFP4, K_stage 256) FLOP/clock/SIMD, which
   is 2048 cycles for every type and for both wave counts;
 * MFMA efficiency = ideal / loop (per SIMD, the figure the reference quotes);
-* clock = shader cycles / 100 MHz ticks over the kernel.
+* clock = shader cycles / 100 MHz ticks over the kernel: the effective shader
+  clock.  (s_memtime counts shader cycles: an MFMA stream on an idle chip
+  reads 2.40 GHz, the part's peak clock.)
+
+Measurements are taken at steady state: operands rotating over >= 512 MiB of
+sets and the kernel running back to back for a settle time first.  A single
+launch on an idle chip runs at a higher clock, where memory latency costs
+more cycles; under sustained load the kernels run at 1.6-2.2 GHz.
 
 Usage (on a GPU box, after ``python -m gfx950_gluon_tutorials_amd.build
 --timing``)::
@@ -94,8 +101,23 @@ def _inputs(dtype: str, M: int, N: int, K: int, dev, seed: int = 0):
     return pa, pb, sa, sb, torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
 
-def measure(dtype: str, M: int, N: int, K: int, waves: int, warmup: int = 20) -> dict:
+def _set_bytes(dtype: str, M: int, N: int, K: int) -> int:
+    if dtype in ("fp16", "bf16"):
+        return (M * K + N * K + M * N) * 2
+    if dtype == "bf8":
+        return M * K + N * K + 2 * M * N
+    return (M * K + N * K) // 2 + (M + N) * K // 32 + 2 * M * N
+
+
+def measure(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.8, rotate_mb: int = 512) -> dict:
+    """Phase statistics of one launch at steady state: the operands rotate
+    over sets of >= rotate_mb MiB (cold caches, as in the benchmark) and the
+    kernel runs back to back for settle_s seconds first, so the clocks have
+    settled (a single launch on an idle chip runs at a higher clock and sees
+    its memory latency as fewer cycles).  Also returns the average launch time
+    of 40 launches just before the stamped one."""
     import ctypes
+    import time
 
     import torch
 
@@ -108,24 +130,42 @@ def measure(dtype: str, M: int, N: int, K: int, waves: int, warmup: int = 20) ->
     lib.g9_timing_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     lib.g9_timing_capacity.restype = ctypes.c_int
     dev = torch.device("cuda:0")
-    x = _inputs(dtype, M, N, K, dev)
-    if dtype in ("fp16", "bf16"):
-        run = lambda: _launch.gemm_a16w16(x[0], x[1], x[2], waves=waves)
-    elif dtype == "bf8":
-        run = lambda: _launch.gemm_a8w8(x[0], x[1], x[2], a_scale=x[3], b_scale=x[4], waves=waves)
-    else:
-        run = lambda: _launch.gemm_a4w4(x[0], x[1], x[2], x[3], x[4], waves=waves)
-    for _ in range(warmup):
-        run()
+    nsets = max(2, -(-rotate_mb * 2**20 // _set_bytes(dtype, M, N, K)))
+    sets = [_inputs(dtype, M, N, K, dev, seed) for seed in range(nsets)]
+
+    def run(i):
+        x = sets[i % nsets]
+        if dtype in ("fp16", "bf16"):
+            _launch.gemm_a16w16(x[0], x[1], x[2], waves=waves)
+        elif dtype == "bf8":
+            _launch.gemm_a8w8(x[0], x[1], x[2], a_scale=x[3], b_scale=x[4], waves=waves)
+        else:
+            _launch.gemm_a4w4(x[0], x[1], x[2], x[3], x[4], waves=waves)
+
+    i = 0
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            run(i)
+            i += 1
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(40):
+        run(i)
+        i += 1
+    e1.record()
     torch.cuda.synchronize()
-    run()
+    launch_us = e0.elapsed_time(e1) / 40 * 1e3
+    run(i)
     torch.cuda.synchronize()
     tiles = -(-M // 256) * -(-N // 256)
     n = min(tiles, lib.g9_timing_capacity())
     buf = np.zeros(n * 8, dtype=np.uint64)
     _lib.check(lib.g9_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_timing_read")
     out = phase_stats(buf, K // STAGE_K[dtype])
-    out.update({"dtype": dtype, "M": M, "N": N, "K": K, "waves": waves})
+    out.update({"dtype": dtype, "M": M, "N": N, "K": K, "waves": waves, "launch_us": round(launch_us, 2),
+                "tflops": round(2.0 * M * N * K / launch_us / 1e6, 1), "rotating_sets": nsets})
     return out
 
 
@@ -144,8 +184,9 @@ def main(argv=None) -> int:
             for w in (int(v) for v in args.waves.split(",")):
                 r = measure(dt, args.M, args.N, K, w)
                 results.append(r)
-                print(f"{dt:6s} {args.M}x{args.N}x{K} waves={w}: MFMA eff {r['mfma_efficiency']:.3f}  "
-                      f"clock {r['clock_ghz']:.3f} GHz  span {r['span_us']:.1f} us  prologue {r['prologue_cycles']}  "
+                print(f"{dt:6s} {args.M}x{args.N}x{K} waves={w}: {r['launch_us']:.1f} us/launch "
+                      f"({r['tflops']:.0f} TFLOPS)  loop MFMA eff {r['mfma_efficiency']:.3f}  "
+                      f"clock {r['clock_ghz']:.3f} GHz  prologue {r['prologue_cycles']}  "
                       f"loop {r['loop_cycles']} (ideal {r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles",
                       flush=True)
     if args.json:
