@@ -13,18 +13,19 @@
 // 256 fp4 values.  A stage is split into four LDS sub-buffers of 128 rows x 128
 // bytes (A rows 0-127 "A0", A rows 128-255 "A1", B rows 0-127 "B0", B rows
 // 128-255 "B1"), each double buffered (two slots), 128 KiB in total.  FP4 adds
-// E8M0 scale sub-buffers of 128 rows x 8 bytes next to them.
+// two slots of E8M0 scale chunks (4 stages of every tile row's scales each).
 //
 // Per stage every wave runs four "quadrant regions" in the order
 // Q00 (A0 x B0), Q01 (A0 x B1), Q11 (A1 x B1), Q10 (A1 x B0).  Each region
 // issues its MFMAs on operand fragments already in registers, reads the next
 // region's operand set from LDS into registers, and refills, by LDS-DMA, the
 // sub-buffer whose last reads finished in the previous region.  A region
-// starts with `s_waitcnt vmcnt(6 groups) lgkmcnt(0)`, issues its first MFMAs,
-// then `s_barrier`: the sub-buffer read during a region was requested seven
-// regions earlier, so the DMA latency budget is 1.5 stages and one barrier per
-// region suffices.  The B operand registers alternate roles between even and
-// odd stages, so the loop body covers two stages.
+// starts with `s_waitcnt vmcnt(N) lgkmcnt(0)` (N: the DMAs issued since the
+// ones it needs), issues its first MFMAs, then `s_barrier`: the sub-buffer read
+// during a region was requested seven regions earlier, so the DMA latency
+// budget is 1.5 stages and one barrier per region suffices.  The B operand
+// registers alternate roles between even and odd stages, so the loop body
+// covers two stages (eight for FP4: two scale chunks).
 //
 // LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk slot
 // c ^ ((r >> 1) & 7).  A ds_read_b128 by 16 consecutive lanes (16 rows, one
