@@ -66,8 +66,46 @@ G9_DEV void timing_stamp(int slot) {
   }
   __builtin_amdgcn_sched_barrier(0);
 }
+// Stream-K phase accounting (timing build): per persistent workgroup, the
+// shader cycles spent waiting for predecessor flags, loading partial tiles
+// (until they are in the accumulators) and storing them (until the release
+// fence has drained the stores), and how many of each.  Slots: 0/1 clock and
+// 100 MHz clock at entry, 2/3 at exit, 4 wait, 5 load, 6 store cycles, 7
+// (loads << 32) | stores.
+struct SkTimes {
+  unsigned long long wait = 0, load = 0, store = 0;
+  unsigned nl = 0, ns = 0;
+};
+G9_DEV unsigned long long clk() {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memtime();
+  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));  // lgkmcnt(0) only
+  __builtin_amdgcn_sched_barrier(0);
+  return t;
+}
+G9_DEV void sk_stamp(int slot) {
+  const unsigned long long t = clk();
+  const unsigned long long r = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));
+  if (threadIdx.x == 0 && blockIdx.x < kTimingTiles) {
+    g9_timing_buf[blockIdx.x * 8 + slot] = t;
+    g9_timing_buf[blockIdx.x * 8 + slot + 1] = r;
+  }
+}
+G9_DEV void sk_times_store(const SkTimes& t) {
+  if (threadIdx.x == 0 && blockIdx.x < kTimingTiles) {
+    g9_timing_buf[blockIdx.x * 8 + 4] = t.wait;
+    g9_timing_buf[blockIdx.x * 8 + 5] = t.load;
+    g9_timing_buf[blockIdx.x * 8 + 6] = t.store;
+    g9_timing_buf[blockIdx.x * 8 + 7] = ((unsigned long long)t.nl << 32) | t.ns;
+  }
+}
 #else
 G9_DEV void timing_stamp(int) {}
+struct SkTimes {};
+G9_DEV unsigned long long clk() { return 0; }
+G9_DEV void sk_stamp(int) {}
+G9_DEV void sk_times_store(const SkTimes&) {}
 #endif
 
 enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3 };
@@ -923,7 +961,7 @@ G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
 }
 
 template <Op OP, int OUT, class G>
-G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se) {
+G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se, SkTimes& times) {
   int tm, tn;
   tile_coords(tile, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, 1, p.group_m, tm, tn);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -932,7 +970,9 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
   if (sb == 0) {
     zero_acc<G>(acc);
   } else {
+    [[maybe_unused]] const unsigned long long t0 = clk();
     wait_flag(p, tile, (p.epoch << 16) | (u32)sb);
+    [[maybe_unused]] const unsigned long long t1 = clk();
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -940,6 +980,13 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
 #pragma unroll
         for (int j = 0; j < G::FN; ++j)
           acc[q >> 1][q & 1][i][j] = load_quads<accv<G>>(ws + ws_index<G>(wave, q, i, j, 0, lane));
+#ifdef G9_TIMING
+    pin_acc<G>(acc);
+    const unsigned long long t2 = clk();
+    times.wait += t1 - t0;
+    times.load += t2 - t1;
+    times.nl += 1;
+#endif
   }
   pin_acc<G>(acc);
   mainloop<OP, G>(p, smem, tm, tn, sb, se, acc);
@@ -947,6 +994,7 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
     store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
     if (sb != 0 && tid == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
+    [[maybe_unused]] const unsigned long long t3 = clk();
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -958,6 +1006,11 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
             ws[ws_index<G>(wave, q, i, j, b, lane)] = get_quad<b>(acc[q >> 1][q & 1][i][j]);
           });
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#ifdef G9_TIMING
+    __builtin_amdgcn_s_waitcnt(0);
+    times.store += clk() - t3;
+    times.ns += 1;
+#endif
     barrier();
     if (tid == 0)
       __hip_atomic_store(p.flags + tile, (p.epoch << 16) | (u32)se, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -981,14 +1034,18 @@ G9_DEV void gemm_sk(const GemmParams& p) {
   const long long base = total / G_, rem = total % G_;
   const long long u0 = cta * base + min((long long)cta, rem);
   long long u1 = u0 + base + (cta < rem ? 1 : 0);
+  SkTimes times;
+  sk_stamp(0);
   while (u1 > u0) {
     const int tile = __builtin_amdgcn_readfirstlane((int)((u1 - 1) / ipt));
     const long long t0 = (long long)tile * ipt;
     const int sb = __builtin_amdgcn_readfirstlane((int)(max(u0, t0) - t0));
     const int se = __builtin_amdgcn_readfirstlane((int)(u1 - t0));
-    sk_segment<OP, OUT, G>(p, smem, tile, sb, se);
+    sk_segment<OP, OUT, G>(p, smem, tile, sb, se, times);
     u1 = t0 + sb;
   }
+  sk_stamp(2);
+  sk_times_store(times);
 }
 
 }  // namespace g9

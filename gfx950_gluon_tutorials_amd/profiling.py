@@ -169,6 +169,84 @@ def measure(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.
     return out
 
 
+def sk_stats(stamps: np.ndarray, M: int, N: int, stage_k: int, K: int) -> dict:
+    """Summarises stream-K stamps (persistent workgroups x 8 uint64: clock and
+    100 MHz clock at entry and exit, flag-wait / partial-load / partial-store
+    cycles, (loads << 32) | stores) into the fixup's cost and bandwidth."""
+    d = np.asarray(stamps, dtype=np.uint64).reshape(-1, 8).astype(np.int64)
+    span = d[:, 2] - d[:, 0]
+    ticks = d[:, 3] - d[:, 1]
+    if (span <= 0).any() or (ticks <= 0).any():
+        raise ValueError("stamps are not increasing: was the last launch a stream-K launch of the timing build?")
+    clock = float(np.median(span / (ticks / REALTIME_HZ)))
+    nl = d[:, 7] >> 32
+    ns = d[:, 7] & 0xFFFFFFFF
+    tile_bytes = 256 * 256 * 4
+    moved = int((nl.sum() + ns.sum()) * tile_bytes)
+    fix = d[:, 5] + d[:, 6]
+    per_load_us = float(d[:, 5].sum() / max(1, nl.sum()) / clock * 1e6)
+    per_store_us = float(d[:, 6].sum() / max(1, ns.sum()) / clock * 1e6)
+    active = fix > 0
+    return {
+        "workgroups": int(d.shape[0]),
+        "clock_ghz": round(clock / 1e9, 4),
+        "span_us": round(float(d[:, 3].max() - d[:, 1].min()) / REALTIME_HZ * 1e6, 2),
+        "partial_loads": int(nl.sum()),
+        "partial_stores": int(ns.sum()),
+        "fixup_bytes": moved,
+        "load_us_per_partial": round(per_load_us, 3),
+        "store_us_per_partial": round(per_store_us, 3),
+        # Each partial is 256 KiB; one workgroup moves it at this rate ...
+        "per_cu_gbs": round(tile_bytes / ((per_load_us + per_store_us) / 2 * 1e-6) / 1e9, 1),
+        # ... and the workgroups that hand off do so at about the same time
+        # (segment starts and ends), so this is the aggregate during fixups.
+        "aggregate_gbs": round(moved / (float(np.mean(fix[active])) / clock) / 1e9, 1) if active.any() else 0.0,
+        "wait_frac": round(float(d[:, 4].sum() / span.sum()), 4),
+        "fixup_frac": round(float(fix.sum() / span.sum()), 4),
+    }
+
+
+def measure_sk(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.8) -> dict:
+    """Stream-K fixup cost at steady state (timing build): how long partial
+    tiles take to store and reload, their bandwidth, and the share of time
+    spent waiting for predecessors."""
+    import ctypes
+    import time
+
+    import torch
+
+    from . import _lib
+    from .gemm import _launch
+
+    lib = _lib.load()
+    if not hasattr(lib, "g9_timing_read"):
+        raise RuntimeError(f"{_lib.LIB_PATH} is not the timing build (python -m gfx950_gluon_tutorials_amd.build --timing)")
+    lib.g9_timing_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    dev = torch.device("cuda:0")
+    x = _inputs(dtype, M, N, K, dev)
+    if dtype in ("fp16", "bf16"):
+        run = lambda: _launch.gemm_a16w16(x[0], x[1], x[2], waves=waves, schedule="streamk")
+    elif dtype == "bf8":
+        run = lambda: _launch.gemm_a8w8(x[0], x[1], x[2], a_scale=x[3], b_scale=x[4], waves=waves, schedule="streamk")
+    else:
+        run = lambda: _launch.gemm_a4w4(x[0], x[1], x[2], x[3], x[4], waves=waves, schedule="streamk")
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            run()
+        torch.cuda.synchronize()
+    run()
+    torch.cuda.synchronize()
+    tiles = -(-M // 256) * -(-N // 256)
+    units = tiles * (K // STAGE_K[dtype])
+    n = min(units, lib.g9_streamk_workgroups())
+    buf = np.zeros(n * 8, dtype=np.uint64)
+    _lib.check(lib.g9_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_timing_read")
+    out = sk_stats(buf, M, N, STAGE_K[dtype], K)
+    out.update({"dtype": dtype, "M": M, "N": N, "K": K, "waves": waves, "tiles": tiles})
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--dtypes", default="fp16,bf8,mxfp4")
@@ -177,8 +255,27 @@ def main(argv=None) -> int:
     ap.add_argument("--K", default="8192", help="comma-separated list")
     ap.add_argument("--waves", default="4")
     ap.add_argument("--json", help="also write the results to this file")
+    ap.add_argument("--streamk", action="store_true",
+                    help="stream-K fixup cost instead (give --M/--N/--K; e.g. 8192 1280 8192)")
     args = ap.parse_args(argv)
     results = []
+    if args.streamk:
+        for dt in args.dtypes.split(","):
+            for K in (int(k) for k in args.K.split(",")):
+                for w in (int(v) for v in args.waves.split(",")):
+                    r = measure_sk(dt, args.M, args.N, K, w)
+                    results.append(r)
+                    print(f"stream-K {dt:6s} {args.M}x{args.N}x{K} waves={w}: {r['workgroups']} workgroups, "
+                          f"{r['tiles']} tiles, span {r['span_us']:.1f} us at {r['clock_ghz']:.2f} GHz; "
+                          f"{r['partial_stores']} partial stores + {r['partial_loads']} loads = "
+                          f"{r['fixup_bytes'] / 2**20:.0f} MiB; per 256 KiB partial: store {r['store_us_per_partial']:.2f} us, "
+                          f"load {r['load_us_per_partial']:.2f} us ({r['per_cu_gbs']:.0f} GB/s per CU, "
+                          f"~{r['aggregate_gbs']:.0f} GB/s aggregate); time in flag waits {100 * r['wait_frac']:.1f}%, "
+                          f"in fixups {100 * r['fixup_frac']:.1f}%", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(results, f, indent=1)
+        return 0
     for dt in args.dtypes.split(","):
         for K in (int(k) for k in args.K.split(",")):
             for w in (int(v) for v in args.waves.split(",")):

@@ -13,11 +13,14 @@
 extern "C" {
 #endif
 
-/* Copies the first `bytes` of the stamp buffer to host memory: per data-
- * parallel workgroup (by block index), 8 uint64 = (shader clock, 100 MHz
- * clock) at kernel entry, main-loop start, main-loop end and kernel end, as
- * left by the last DP launch.  Synchronous.  Returns G9_OK, G9_ERR_SHAPE when
- * `bytes` exceeds the buffer, or G9_ERR_HIP. */
+/* Copies the first `bytes` of the stamp buffer to host memory, as left by the
+ * last launch, 8 uint64 per workgroup (by block index).  Data-parallel:
+ * (shader clock, 100 MHz clock) at kernel entry, main-loop start, main-loop
+ * end and kernel end.  Stream-K: (shader clock, 100 MHz clock) at entry and
+ * exit, then shader cycles spent waiting for predecessor flags, loading
+ * partial tiles and storing them, and (partial loads << 32) | partial stores.
+ * Synchronous.  Returns G9_OK, G9_ERR_SHAPE when `bytes` exceeds the buffer,
+ * or G9_ERR_HIP. */
 int g9_timing_read(void* host, size_t bytes);
 
 /* Number of workgroups the buffer holds stamps for. */

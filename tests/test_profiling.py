@@ -39,3 +39,23 @@ def test_rejects_stamps_from_another_launch():
     bad[:, 4] = bad[:, 2] - 5  # loop end before loop start
     with pytest.raises(ValueError):
         profiling.phase_stats(bad, 64)
+
+
+def test_sk_stats_bandwidth_and_fractions():
+    # 4 workgroups, each: 200000 shader cycles over 10000 ticks of 100 MHz (2 GHz), one partial
+    # load of 20000 cycles (10 us) and one store of 30000 (15 us), 5000 cycles of flag waits.
+    d = np.zeros((4, 8), dtype=np.uint64)
+    for i in range(4):
+        d[i] = [1000, 10, 1000 + 200000, 10 + 10000, 5000, 20000, 30000, (1 << 32) | 1]
+    r = profiling.sk_stats(d.ravel(), 256, 256, 64, 8192)
+    assert r["clock_ghz"] == 2.0
+    assert r["partial_loads"] == 4 and r["partial_stores"] == 4
+    assert r["fixup_bytes"] == 8 * 256 * 256 * 4
+    assert r["load_us_per_partial"] == 10.0 and r["store_us_per_partial"] == 15.0
+    assert r["per_cu_gbs"] == round(262144 / 12.5e-6 / 1e9, 1)
+    assert r["wait_frac"] == 0.025 and r["fixup_frac"] == 0.25
+
+
+def test_sk_stats_rejects_stamps_of_another_launch():
+    with pytest.raises(ValueError):
+        profiling.sk_stats(np.zeros(16, dtype=np.uint64), 256, 256, 64, 8192)
