@@ -70,6 +70,8 @@ def phase_stats(stamps: np.ndarray, stages: int) -> dict:
         "clock_ghz": round(float(np.median(clock)) / 1e9, 4),
         "span_us": round(float(r[:, 3].max() - r[:, 0].min()) / REALTIME_HZ * 1e6, 2),
         "start_skew_us": round(float(r[:, 0].max() - r[:, 0].min()) / REALTIME_HZ * 1e6, 3),
+        "workgroup_us": round(float(np.median(ticks)) / REALTIME_HZ * 1e6, 2),
+        "end_spread_us": round(float(r[:, 3].max() - np.median(r[:, 3])) / REALTIME_HZ * 1e6, 3),
         "prologue_cycles": int(np.median(pro)),
         "loop_cycles": int(loop_med),
         "loop_cycles_min": int(loop.min()),
@@ -284,7 +286,9 @@ def main(argv=None) -> int:
                 print(f"{dt:6s} {args.M}x{args.N}x{K} waves={w}: {r['launch_us']:.1f} us/launch "
                       f"({r['tflops']:.0f} TFLOPS)  loop MFMA eff {r['mfma_efficiency']:.3f}  "
                       f"clock {r['clock_ghz']:.3f} GHz  prologue {r['prologue_cycles']}  "
-                      f"loop {r['loop_cycles']} (ideal {r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles",
+                      f"loop {r['loop_cycles']} (ideal {r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles  "
+                      f"| workgroup {r['workgroup_us']:.1f} us, span {r['span_us']:.1f} us (start skew "
+                      f"{r['start_skew_us']:.2f}, last end +{r['end_spread_us']:.2f} after the median)",
                       flush=True)
     if args.json:
         with open(args.json, "w") as f:
