@@ -249,6 +249,86 @@ def measure_sk(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float =
     return out
 
 
+OPERAND_KINDS = ("randn", "zeros", "a_const", "b_const", "sign_only", "k_const")
+
+
+def _study_operands(kind: str, M: int, N: int, K: int, g):
+    import torch
+
+    def rnd(rows):
+        return torch.randn(rows, K, generator=g) * 0.1
+
+    if kind == "randn":
+        a, b = rnd(M), rnd(N)
+    elif kind == "zeros":
+        a, b = torch.zeros(M, K), torch.zeros(N, K)
+    elif kind == "a_const":  # A = 0.1 everywhere (the MFMAs' second operand), B random
+        a, b = torch.full((M, K), 0.1), rnd(N)
+    elif kind == "b_const":  # B = 0.1 everywhere (the MFMAs' first operand), A random
+        a, b = rnd(M), torch.full((N, K), 0.1)
+    elif kind == "sign_only":  # +-0.1 with random signs: only the sign bits vary
+        a = (torch.randint(0, 2, (M, K), generator=g) * 0.2 - 0.1)
+        b = (torch.randint(0, 2, (N, K), generator=g) * 0.2 - 0.1)
+    elif kind == "k_const":  # every row constant along K
+        a = (torch.randn(M, 1, generator=g) * 0.1).expand(M, K).contiguous()
+        b = (torch.randn(N, 1, generator=g) * 0.1).expand(N, K).contiguous()
+    else:
+        raise ValueError(f"unknown operand kind {kind!r}; choose from {OPERAND_KINDS}")
+    return a.half(), b.half()
+
+
+def operand_study(kinds, M: int = 4096, N: int = 4096, K: int = 8192, waves: int = 4, settle_s: float = 1.0,
+                  nsets: int = 4) -> list:
+    """Launch time of the FP16 data-parallel kernel on differently distributed
+    operands.  The instruction stream and the memory traffic are the same for
+    every kind; only the values differ, so under the board's power limit the
+    differences are the data-dependent part of the energy per launch.  Each
+    kind runs back to back for settle_s seconds before 8 timed batches of 40
+    launches (median)."""
+    import time
+
+    import torch
+
+    from .gemm import _launch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(7)
+    out = []
+    for kind in kinds:
+        sets = []
+        for _ in range(nsets):
+            a, b = _study_operands(kind, M, N, K, g)
+            sets.append((a.to(dev), b.to(dev).T, torch.empty(M, N, dtype=torch.float16, device=dev)))
+
+        def run(i):
+            x = sets[i % nsets]
+            _launch.gemm_a16w16(x[0], x[1], x[2], waves=waves)
+
+        i = 0
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                run(i)
+                i += 1
+            torch.cuda.synchronize()
+        times = []
+        for _ in range(8):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(40):
+                run(i)
+                i += 1
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / 40 * 1e3)
+        us = float(np.median(times))
+        out.append({"kind": kind, "M": M, "N": N, "K": K, "waves": waves, "launch_us": round(us, 2),
+                    "tflops": round(2.0 * M * N * K / us / 1e6, 1)})
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--dtypes", default="fp16,bf8,mxfp4")
@@ -259,8 +339,20 @@ def main(argv=None) -> int:
     ap.add_argument("--json", help="also write the results to this file")
     ap.add_argument("--streamk", action="store_true",
                     help="stream-K fixup cost instead (give --M/--N/--K; e.g. 8192 1280 8192)")
+    ap.add_argument("--operands", help="FP16 launch time per operand distribution instead "
+                    f"(comma-separated from {','.join(OPERAND_KINDS)})")
     args = ap.parse_args(argv)
     results = []
+    if args.operands:
+        for w in (int(v) for v in args.waves.split(",")):
+            for r in operand_study(args.operands.split(","), args.M, args.N, int(args.K.split(",")[0]), w):
+                results.append(r)
+                print(f"fp16 {args.M}x{args.N}x{r['K']} waves={w} operands {r['kind']:10s}: "
+                      f"{r['launch_us']:.1f} us/launch ({r['tflops']:.0f} TFLOPS)", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(results, f, indent=1)
+        return 0
     if args.streamk:
         for dt in args.dtypes.split(","):
             for K in (int(k) for k in args.K.split(",")):

@@ -59,3 +59,18 @@ def test_sk_stats_bandwidth_and_fractions():
 def test_sk_stats_rejects_stamps_of_another_launch():
     with pytest.raises(ValueError):
         profiling.sk_stats(np.zeros(16, dtype=np.uint64), 256, 256, 64, 8192)
+
+
+def test_operand_study_kinds():
+    import torch
+
+    g = torch.Generator().manual_seed(0)
+    for kind in profiling.OPERAND_KINDS:
+        a, b = profiling._study_operands(kind, 32, 16, 64, g)
+        assert a.shape == (32, 64) and b.shape == (16, 64) and a.dtype == b.dtype == torch.float16
+    a, b = profiling._study_operands("b_const", 8, 8, 32, g)
+    assert torch.all(b == b[0, 0]) and a.unique().numel() > 1
+    a, b = profiling._study_operands("k_const", 8, 8, 32, g)
+    assert torch.all(a == a[:, :1]) and torch.all(b == b[:, :1])
+    with pytest.raises(ValueError):
+        profiling._study_operands("uniform", 8, 8, 32, g)
