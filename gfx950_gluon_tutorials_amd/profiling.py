@@ -47,6 +47,7 @@ import numpy as np
 CYCLES_PER_STAGE = 2048
 STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256}
 REALTIME_HZ = 100e6
+NUM_XCDS = 8
 
 
 def phase_stats(stamps: np.ndarray, stages: int) -> dict:
@@ -64,6 +65,12 @@ def phase_stats(stamps: np.ndarray, stages: int) -> dict:
     clock = (t[:, 3] - t[:, 0]) / (ticks / REALTIME_HZ)
     ideal = stages * CYCLES_PER_STAGE
     loop_med = float(np.median(loop))
+    # Workgroups are dispatched round-robin over the XCDs (workgroup i runs on
+    # XCD i % 8 of an MI355X); each XCD runs at its own clock.
+    xcds = min(NUM_XCDS, d.shape[0])
+    xcd = np.arange(d.shape[0]) % xcds
+    xcd_clock = [float(np.median(clock[xcd == x])) / 1e9 for x in range(xcds)]
+    xcd_end = [float(np.median(r[xcd == x, 3] - r[:, 0].min())) / REALTIME_HZ * 1e6 for x in range(xcds)]
     return {
         "workgroups": int(d.shape[0]),
         "stages": stages,
@@ -80,6 +87,8 @@ def phase_stats(stamps: np.ndarray, stages: int) -> dict:
         "ideal_loop_cycles": ideal,
         "mfma_efficiency": round(ideal / loop_med, 4),
         "loop_fraction": round(loop_med / float(np.median(t[:, 3] - t[:, 0])), 4),
+        "xcd_clock_ghz": [round(c, 3) for c in xcd_clock],
+        "xcd_end_us": [round(e, 2) for e in xcd_end],
     }
 
 
@@ -380,7 +389,9 @@ def main(argv=None) -> int:
                       f"clock {r['clock_ghz']:.3f} GHz  prologue {r['prologue_cycles']}  "
                       f"loop {r['loop_cycles']} (ideal {r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles  "
                       f"| workgroup {r['workgroup_us']:.1f} us, span {r['span_us']:.1f} us (start skew "
-                      f"{r['start_skew_us']:.2f}, last end +{r['end_spread_us']:.2f} after the median)",
+                      f"{r['start_skew_us']:.2f}, last end +{r['end_spread_us']:.2f} after the median) | per-XCD clock "
+                      f"{min(r['xcd_clock_ghz']):.3f}-{max(r['xcd_clock_ghz']):.3f} GHz, median end "
+                      f"{min(r['xcd_end_us']):.1f}-{max(r['xcd_end_us']):.1f} us",
                       flush=True)
     if args.json:
         with open(args.json, "w") as f:

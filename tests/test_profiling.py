@@ -28,6 +28,20 @@ def test_efficiency_and_clock():
     assert s["loop_cycles_max"] - s["loop_cycles_min"] == 30
 
 
+def test_per_xcd_clock_and_end():
+    # 16 workgroups: the odd ones (XCDs 1, 3, 5, 7) run at 1.2 GHz, the even ones at 1.5 GHz.
+    stages = 64
+    loop = stages * profiling.CYCLES_PER_STAGE
+    fast = _stamps(1000, loop, 1000, clock_hz=1.5e9, n=16)
+    slow = _stamps(1000, loop, 1000, clock_hz=1.2e9, n=16)
+    d = np.where((np.arange(16) % 2 == 1)[:, None], slow, fast)
+    s = profiling.phase_stats(d, stages)
+    assert len(s["xcd_clock_ghz"]) == profiling.NUM_XCDS == 8
+    assert all(abs(c - (1.2 if x % 2 else 1.5)) < 0.01 for x, c in enumerate(s["xcd_clock_ghz"]))
+    cycles = 1000 + loop + 1000
+    assert abs(s["xcd_end_us"][1] - cycles / 1.2e3) < 1.0 and abs(s["xcd_end_us"][0] - cycles / 1.5e3) < 1.0
+
+
 def test_cycles_per_stage_matches_the_mfma_rates():
     # 256x256 tile, K per stage, over 4 SIMDs at the dtype's FLOP/clock/SIMD.
     for dt, flop_per_clk in (("fp16", 1024), ("bf16", 1024), ("bf8", 2048), ("mxfp4", 4096)):
