@@ -422,8 +422,9 @@ def main():
         torch.cuda.empty_cache()
     sk = {}
     if args.streamk and not args.only:
-        for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192)]:
-            launch = make_case("fp16", m, n, k, 4, dev, 2)
+        # The BASELINE shapes (fewer tiles than CUs), then two with more: 272 and 400 tiles.
+        for (m, n, k) in [(3840, 3840, 16384), (8192, 1280, 8192), (4352, 4096, 8192), (5120, 5120, 8192)]:
+            launch = make_case("fp16", m, n, k, 4, dev, max(2, -(-args.rotate_mb * 2**20 // set_bytes("fp16", m, n, k))))
             ms_dp = time_case(launch, max(10, args.steps // 2), args.warmup, "dp", args.settle_ms / 2e3)
             ms_sk = time_case(launch, max(10, args.steps // 2), args.warmup, "streamk", args.settle_ms / 2e3)
             flop = 2.0 * m * n * k

@@ -253,9 +253,11 @@ def test_a8w8_stage_counts(gpu, ns, waves):
     np.testing.assert_array_equal(_bits(outs["streamk"]), _bits(outs["dp"]))
 
 
-@pytest.mark.parametrize("M,N,K", [(3840, 3840, 16384), (8192, 1280, 8192)])
+@pytest.mark.parametrize("M,N,K", [(3840, 3840, 16384), (8192, 1280, 8192), (4352, 4096, 1024), (5120, 5120, 2048)])
 def test_streamk_bit_identical_to_dp(gpu, M, N, K):
-    """fp16 randn(seed=4)*0.1; stream-K output == data-parallel output, bit for bit."""
+    """fp16 randn(seed=4)*0.1; stream-K output == data-parallel output, bit for bit.  The
+    last two shapes have more tiles than workgroups (272 and 400 tiles), so workgroups own a tile's
+    suffix, whole tiles and the next tile's prefix."""
     _say(f"stream-K vs DP {M}x{N}x{K} seed4")
     gen = torch.Generator().manual_seed(4)
     a = _randn(gen, (M, K), 0.1).half().to(gpu)
