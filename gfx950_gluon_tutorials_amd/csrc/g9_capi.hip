@@ -2,7 +2,6 @@
 // include/gfx950_gemm.h).  Each validates shapes, strides and alignment,
 // fills a GemmParams and launches one named kernel on the caller's stream.
 #include <atomic>
-#include <mutex>
 
 #include "../../include/gfx950_gemm.h"
 #include "g9_gemm.hpp"
@@ -91,16 +90,16 @@ size_t flags_bytes(long long tiles) { return align256((size_t)tiles * 4); }
 
 std::atomic<unsigned> g_epoch{0};
 
+// CUs of the current device (cached per device; 0 if it cannot be queried).
 int cu_count() {
-  static std::once_flag once;
-  static int cus = 0;
-  std::call_once(once, [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cus = n;
-  });
-  return cus;
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices && (n = cache[dev].load(std::memory_order_relaxed)) > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+  if (dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -136,14 +135,20 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     grid = (int)(units < cus ? units : cus);
     p.sk_ctas = grid;
   }
-  hipLaunchKernelGGL(k->fn, dim3(grid), dim3(64 * waves), 0, s, p);
-  return hipGetLastError() == hipSuccess ? G9_OK : G9_ERR_HIP;
+  // hipLaunchKernel reports this launch's own status (hipGetLastError would
+  // also return an earlier, unrelated error of the calling thread).
+  void* args[] = {&p};
+  return hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3(grid), dim3(64 * waves), args, 0, s) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
                  const void* c) {
   if (M <= 0 || N <= 0 || K <= 0) return G9_ERR_SHAPE;
   if (M > (1 << 30) || N > (1 << 30)) return G9_ERR_SHAPE;
+  // Tile ids and the data-parallel grid are 32-bit.
+  if (((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile) > INT32_MAX) return G9_ERR_SHAPE;
   const int sk = stage_k(dtype);
   if (K % sk != 0 || K / sk >= 65536) return G9_ERR_SHAPE;
   if (stride_cn != 1 || stride_cm < N || !aligned(c, 2)) return G9_ERR_LAYOUT;
@@ -266,17 +271,21 @@ extern "C" {
 
 int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   if (!workspace || workspace_bytes < kWsHeader || !aligned(workspace, 256)) return G9_ERR_WORKSPACE;
-  // Header and flags precede the partial tiles; clearing everything up to the
-  // first tile covers both (bounded by the workspace size).
-  size_t words = workspace_bytes / 4;
-  // Flags of at most 2^20 tiles: far beyond any supported shape.
-  const size_t cap = (kWsHeader + flags_bytes(1 << 20)) / 4;
-  if (words > cap) words = cap;
+  // Header and flags precede the partial tiles.  Clear the flags of the
+  // largest tile count whose partials fit this workspace, so every launch the
+  // workspace is large enough for finds its flags cleared.
+  const size_t max_tiles = (workspace_bytes - kWsHeader) / kWsTileBytes + 1;
+  size_t words = (kWsHeader + flags_bytes((long long)max_tiles)) / 4;
+  if (words > workspace_bytes / 4) words = workspace_bytes / 4;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int threads = 256;
   const int blocks = (int)((words + threads - 1) / threads);
-  hipLaunchKernelGGL(zero_words, dim3(blocks), dim3(threads), 0, s, static_cast<u32*>(workspace), words);
-  return hipGetLastError() == hipSuccess ? G9_OK : G9_ERR_HIP;
+  u32* w = static_cast<u32*>(workspace);
+  void* args[] = {&w, &words};
+  return hipLaunchKernel(reinterpret_cast<const void*>(zero_words), dim3(blocks), dim3(threads), args, 0, s) ==
+                 hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
 }
 
 int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stream, int* error) {

@@ -88,6 +88,8 @@ def _a16w16(M=512, N=512, K=1024, sam=None, sak=1, sbk=1, sbn=None, scm=None, sc
     (dict(N=-5), _lib.G9_ERR_SHAPE),
     (dict(K=100), _lib.G9_ERR_SHAPE),
     (dict(K=0), _lib.G9_ERR_SHAPE),
+    (dict(M=(1 << 30) + 1), _lib.G9_ERR_SHAPE),
+    (dict(M=1 << 30, N=1 << 30), _lib.G9_ERR_SHAPE),  # 2^44 tiles: tile ids are 32-bit
     (dict(sak=2), _lib.G9_ERR_LAYOUT),
     (dict(sbk=1024, sbn=1), _lib.G9_ERR_LAYOUT),
     (dict(scn=2), _lib.G9_ERR_LAYOUT),
