@@ -179,7 +179,7 @@ struct Geo {
   // Row chunk held as the lane's chunk r by lane group gi.  The same map is
   // used for A and B, so it only permutes K inside a stage.
   //   MD 16: chunk 4r + gi.  16x16 MFMA step r takes K chunk 4r..4r+3 from
-  //          lane groups 0..3, which is the natural K order for FP16/BF16;
+  //          lane groups 0..3, which is the natural K order for FP16/BF16/FP4;
   //          BF8 feeds chunks r = 0, 1 to one MFMA (a K permutation), which
   //          keeps the read pattern of the 16-bit types, free of bank
   //          conflicts (the contiguous chunks 2gi, 2gi + 1 measured 2-way
@@ -188,14 +188,7 @@ struct Geo {
   //          FP4 lane's four E8M0 scales (groups 4gi..4gi+3) are one aligned
   //          dword of its row's eight scale bytes, read without a byte
   //          shuffle.
-  //   FP4 with MD 16 (`scaled`): chunk 2gi + r.  Each 16-byte chunk is one
-  //          32-value scale group, so a lane's scales for steps 0 and 1 are
-  //          the adjacent bytes 2gi, 2gi + 1 of its row's eight: one 16-bit
-  //          LDS read puts them in bytes 0 and 1 of the scale register, which
-  //          the steps select with op_sel (no byte shuffle, no wait for it).
-  static constexpr int chunk(int r, int gi, bool scaled = false) {
-    return MD == 32 ? 4 * gi + r : scaled ? 2 * gi + r : 4 * r + gi;
-  }
+  static constexpr int chunk(int r, int gi) { return MD == 16 ? 4 * r + gi : 4 * gi + r; }
 };
 template <int MD>
 using Geo4 = Geo<4, 2, 2, MD>;
@@ -226,7 +219,8 @@ using Geo8 = Geo<8, 2, 4, MD>;
 template <int NC>
 struct Frag {
   u32x4 c[NC];
-  u32 sp;  // FP4: byte e = scale of the lane's data in MFMA step e
+  u32x2 sc;  // FP4, MD 16: the lane's 8 raw E8M0 bytes of the stage (groups 0..7)
+  u32 sp;    // FP4: byte e = scale of the lane's data in MFMA step e
 };
 
 template <Op OP>
@@ -400,8 +394,10 @@ G9_DEV void static_for(F&& f) {
 // resolves; everything else follows the barrier, placed after MFMA kPre + q
 // for q in [0, NQ).  The region's NR 16-byte LDS reads come first, spread over
 // a window of W slots, so the region-closing lgkmcnt(0) finds them complete;
-// the DMAs are spread over the whole region.  FP4 reads the scale bytes of
-// each fragment after the first reads.
+// the DMAs are spread over the whole region.  FP4 reads one scale word per
+// fragment after the first reads; with 16x16 fragments it then gathers the
+// bytes each MFMA step needs at slot kPermQ, after its reads and well before
+// the next region's MFMAs read the results.
 template <Op OP, class G, int NF>
 struct Slots {
   static constexpr int NM = Shape<OP, G>::NM;
@@ -415,6 +411,9 @@ struct Slots {
   static constexpr int D = G::kDmaPerSub;
   static constexpr int dma_q(int J) { return NQ == 1 ? 0 : 1 + J * (NQ - 1) / D; }
   static constexpr int kScaleDmaQ = dma_q(D - 1) + 2 < NQ ? dma_q(D - 1) + 2 : NQ - 1;
+  static constexpr int kLastQ = (read_q(NR - 1) > scale_q(NF - 1) ? read_q(NR - 1) : scale_q(NF - 1)) + 3;
+  static constexpr int kPermQ = (kLastQ > NQ - 8 ? kLastQ : NQ - 8) < NQ - 1 ? (kLastQ > NQ - 8 ? kLastQ : NQ - 8)
+                                                                              : NQ - 1;
   static_assert(NQ >= 1, "a region needs an MFMA after its barrier");
   static_assert(!OpInfo<OP>::kScaled || scale_q(NF - 1) < NQ, "scale reads must fit the region");
 };
@@ -452,6 +451,7 @@ struct Pipe {
   u32 vS[SP];               // FP4: chunk DMA offsets (32 rows x 32 bytes each)
   u32 bA[G::NC], bB[G::NC];  // LDS read bases of the lane's chunks (A at 0, B at 64 KiB)
   u32 bS[2][2];             // FP4: LDS read bases [A/B][stages 0-1 / 2-3 of a chunk]
+  u32 sel;                  // FP4, MD 16: scale byte selector
   u32 lds0;                 // LDS address of the shared buffer
   u32 mrow;                 // LDS address of the wave's rows in sub-buffer A0, slot 0
   u32 msc;                  // FP4: LDS address of the wave's chunk rows in chunk slot 0
@@ -502,7 +502,7 @@ struct Pipe {
     const int sw = (rr >> 1) & 7;
 #pragma unroll
     for (int c = 0; c < G::NC; ++c) {
-      const int slot = G::chunk(c, gi, I::kScaled) ^ sw;
+      const int slot = G::chunk(c, gi) ^ sw;
       bA[c] = opaque(lds0 + (u32)(wm * G::FM * G::MD + rr) * kRowBytes + slot * 16);
       bB[c] = opaque(lds0 + 65536u + (u32)(wn * G::FN * G::MD + rr) * kRowBytes + slot * 16);
     }
@@ -529,11 +529,11 @@ struct Pipe {
         vS[j] = (u32)row * lds + half * 16;
       }
       msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
-      // Lane group gi reads the scale bytes of its chunks (Geo::chunk): MD 16
-      // the two bytes of groups 2gi, 2gi + 1, MD 32 the dword of groups
-      // 4gi..4gi+3.  Fragment rows are multiples of 16, so the row swap
-      // depends on rr only.
-      const u32 word = G::MD == 32 ? 4u * gi : 2u * gi;
+      // MD 16 reads the row's 8 scale bytes of a stage and picks groups gi
+      // and 4 + gi (byte 0x0c of a v_perm selector yields zero); MD 32 reads
+      // the dword of groups 4gi..4gi+3 directly.  Fragment rows are multiples
+      // of 16, so the row swap depends on rr only.
+      const u32 word = G::MD == 32 ? 4u * gi : 0u;
       const int ssw = (rr >> 3) & 1;
 #pragma unroll
       for (int g = 0; g < (G::NW == 4 ? 2 : 1); ++g) {
@@ -541,6 +541,9 @@ struct Pipe {
         bS[1][g] =
             opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
       }
+      sel = (u32)gi | ((u32)(4 + gi) << 8) | 0x0c0c0000u;
+    } else {
+      sel = 0;
     }
   }
 
@@ -590,7 +593,7 @@ struct Pipe {
       asm volatile("v_xor_b32 %0, 16, %0" : "+v"(base));
     }
     if constexpr (G::MD == 16)
-      f[F].sp = *(const G9_LDS uint16_t*)(uintptr_t)(base + imm);
+      f[F].sc = *(const G9_LDS u32x2*)(uintptr_t)(base + imm);
     else
       f[F].sp = *(const G9_LDS u32*)(uintptr_t)(base + imm);
   }
@@ -616,6 +619,12 @@ struct Pipe {
       [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SSLOT, ST, F>(f), ...); }(
           std::make_integer_sequence<int, NF>{});
     }
+  }
+  template <int X>
+  G9_DEV void gather_scales(FragSet<G>& f) const {
+    constexpr int NF = X < 2 ? G::FM : G::FN;
+#pragma unroll
+    for (int i = 0; i < NF; ++i) f[i].sp = __builtin_amdgcn_perm(f[i].sc.y, f[i].sc.x, sel);
   }
 };
 
@@ -693,6 +702,10 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
       if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
     });
     if constexpr (part >= 0 && q == S::kScaleDmaQ) P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, ms);
+    if constexpr (OpInfo<OP>::kScaled && G::MD == 16 && q == S::kPermQ) {
+      waitcnt<63, 0>();
+      P.template gather_scales<RX>(nxt);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -798,6 +811,10 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   P.template load<0, 0, 0, 0>(at);
   P.template load<2, 0, 0, 0>(x);
   waitcnt<kFirst, 0>();
+  if constexpr (kScaled && G::MD == 16) {
+    P.template gather_scales<0>(at);
+    P.template gather_scales<2>(x);
+  }
   barrier();
   P.template issue<0, 0>(s0 + 2);
   // The accumulators were just written by VALU (zeroing or a partial tile):
