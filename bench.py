@@ -337,11 +337,22 @@ def summarize_rocpd(path: str) -> None:
                 print(f"{name[:48]:48s} {grid:8d} {len(d):6d} {st.mean(d):9.2f} {st.median(d):9.2f} "
                       f"{min(d):8.2f} {max(d):8.2f} {st.mean(d[-100:]):15.2f}")
         if "counters_collection" in views:
-            rows = con.execute("select kernel_name, grid_size, counter_name, value, duration "
-                               "from counters_collection").fetchall()
-            groups = {}
-            for name, grid, cn, val, dur in rows:
-                g = groups.setdefault((name, grid), {"dur": []})
+            cols = {r[1] for r in con.execute("pragma table_info(counters_collection)")}
+            order = next((c for c in ("dispatch_id", "start", "start_time") if c in cols), None)
+            disp = order if order else "0"
+            rows = con.execute(f"select kernel_name, grid_size, counter_name, value, duration, {disp} "
+                               "from counters_collection" + (f" order by {order}" if order else "")).fetchall()
+            # Consecutive runs of a GEMM kernel (one per shape) are grouped
+            # separately, as for the kernel trace: the later ones get #2, #3...
+            groups, runs, last = {}, {}, None
+            for name, grid, cn, val, dur, _ in rows:
+                key = (name, grid)
+                if name.startswith("g9_") and key != last:
+                    runs[key] = runs.get(key, 0) + 1
+                    last = key
+                n = runs.get(key, 1)
+                gname = name if n == 1 else f"{name}#{n}"
+                g = groups.setdefault((gname, grid), {"dur": []})
                 g.setdefault(cn, []).append(val)
                 g["dur"].append(dur / 1e3)
             for (name, grid), g in sorted(groups.items(), key=lambda kv: -sum(kv[1]["dur"])):
