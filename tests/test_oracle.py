@@ -184,7 +184,8 @@ def test_get_pids_is_a_bijection_with_xcd_locality(grid_m, grid_n, xcds, gm):
             assert len(ms) == 4 and len(ns) == 8 and len(tiles) == 32
 
 
-@pytest.mark.parametrize("tiles,stages,ctas", [(225, 256, 256), (160, 128, 256), (4, 7, 3), (3, 5, 16), (10, 2, 7)])
+@pytest.mark.parametrize("tiles,stages,ctas", [(225, 256, 256), (160, 128, 256), (272, 128, 256), (400, 128, 256),
+                                               (4, 7, 3), (3, 5, 16), (10, 2, 7)])
 def test_streamk_partition_covers_every_stage_once(tiles, stages, ctas):
     segs = R.streamk_segments(tiles, stages, ctas)
     count = np.zeros((tiles, stages), dtype=np.int64)
@@ -196,6 +197,15 @@ def test_streamk_partition_covers_every_stage_once(tiles, stages, ctas):
     steps, flags = R.simulate_streamk(tiles, stages, ctas)
     total = tiles * stages
     assert steps >= -(-total // ctas)
+
+
+@pytest.mark.parametrize("tiles,stages,ctas", [(225, 256, 256), (160, 128, 256), (272, 128, 256), (320, 128, 256),
+                                               (400, 128, 256), (512, 128, 256)])
+def test_streamk_makespan_is_one_chain_or_the_even_share(tiles, stages, ctas):
+    # With K-ordered chains a tile's stages run one after another, so the makespan is at least one tile's
+    # chain; with at least a tile per workgroup no workgroup waits and the even share is reached.
+    steps, _ = R.simulate_streamk(tiles, stages, ctas)
+    assert steps == max(stages, -(-tiles * stages // ctas))
 
 
 def test_streamk_segments_run_last_tile_first():
