@@ -127,3 +127,14 @@ def test_status_maps_to_python_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.G9_ERR_HIP, "x")
     _lib.check(_lib.G9_OK, "x")
+
+
+def test_auto_schedule_rule():
+    from gfx950_gluon_tutorials_amd.gemm import _launch
+
+    dp, sk = _lib.G9_SCHED_DP, _lib.G9_SCHED_SK
+    cases = {(3840, 3840): dp, (8192, 1280): dp, (4096, 4096): dp, (4352, 4096): sk, (4096, 5120): sk,
+             (4352, 4864): dp, (5120, 5120): dp, (4097, 4096): sk}
+    for (M, N), want in cases.items():
+        assert _launch.auto_schedule(M, N, cus=256) == want, (M, N)
+    assert _launch.auto_schedule(4352, 4096, cus=0) == dp  # no device: never stream-K

@@ -271,6 +271,21 @@ def test_streamk_bit_identical_to_dp(gpu, M, N, K):
     _check_f16(dp, R.a16w16_ref(a[rows].cpu().numpy(), b.cpu().numpy()), K=K, sigma=0.01, rows=rows)
 
 
+def test_auto_schedule_picks_streamk_at_272_tiles(gpu):
+    _say("schedule=auto 4352x4096x1024")
+    gen = torch.Generator().manual_seed(6)
+    M, N, K = 4352, 4096, 1024
+    a = _randn(gen, (M, K), 0.1).half().to(gpu)
+    b = _randn(gen, (N, K), 0.1).half().to(gpu)
+    if _lib.load().g9_streamk_workgroups() == 256:
+        assert _launch.auto_schedule(M, N) == _lib.G9_SCHED_SK
+    dp = a16w16_matmul(a, b.T, schedule="dp")
+    auto = a16w16_matmul(a, b.T, schedule="auto")
+    torch.cuda.synchronize()
+    _check_streamk_clean(gpu)
+    np.testing.assert_array_equal(_bits(auto), _bits(dp))
+
+
 @pytest.mark.parametrize("kind", ["a8w8", "a4w4", "bf16"])
 def test_streamk_bit_identical_other_dtypes(gpu, kind):
     _say(f"stream-K vs DP {kind}")
