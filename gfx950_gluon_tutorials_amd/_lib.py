@@ -51,6 +51,10 @@ SIGNATURES = {
                             _vp, _vp, _int, _int, _int, _vp, _sz, _vp]),
     "g9_gemm_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]),
+    "g9_moe_a16w16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "g9_moe_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                           _i64, _i64, _int, _vp]),
+    "g9_moe_kernel_name": (ctypes.c_char_p, [_int, _int]),
     "g9_workspace_size": (_sz, [_int, _i64, _i64, _i64, _int, _int]),
     "g9_workspace_init": (_int, [_vp, _sz, _vp]),
     "g9_workspace_error": (_int, [_vp, _sz, _vp, ctypes.POINTER(_int)]),
@@ -104,4 +108,9 @@ def check(code: int, what: str) -> None:
 
 def kernel_name(dtype: int, out_dtype: int, schedule: int, waves: int) -> str | None:
     name = load().g9_kernel_name(dtype, out_dtype, schedule, waves)
+    return name.decode() if name else None
+
+
+def moe_kernel_name(dtype: int, out_dtype: int) -> str | None:
+    name = load().g9_moe_kernel_name(dtype, out_dtype)
     return name.decode() if name else None

@@ -36,6 +36,17 @@ G9_DEFINE(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
 G9_DEFINE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
 G9_DEFINE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
+// Grouped (MoE) kernels, 4-wave.
+#define G9_DEFINE_MOE(NAME, OP, OUT)                                                                \
+  extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_moe_4w(GemmParams p) {                      \
+    gemm_moe<OP, OUT, NAME##_g4>(p);                                                                \
+  }
+
+G9_DEFINE_MOE(g9_a16w16_f16, Op::F16, OUT_F16)
+G9_DEFINE_MOE(g9_a16w16_bf16, Op::BF16, OUT_BF16)
+G9_DEFINE_MOE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
+G9_DEFINE_MOE(g9_a4w4_f16out, Op::FP4, OUT_F16)
+
 typedef void (*KernelFn)(GemmParams);
 
 namespace {
@@ -58,6 +69,19 @@ const KernelEntry kKernels[] = {
     G9_ENTRY(G9_BF8, G9_F16, g9_a8w8_f16out),    G9_ENTRY(G9_BF8, G9_BF16, g9_a8w8_bf16out),
     G9_ENTRY(G9_FP4, G9_BF16, g9_a4w4_bf16out),  G9_ENTRY(G9_FP4, G9_F16, g9_a4w4_f16out),
 };
+
+const KernelEntry kMoeKernels[] = {
+    {G9_F16, G9_F16, G9_SCHED_DP, 4, g9_a16w16_f16_moe_4w, "g9_a16w16_f16_moe_4w"},
+    {G9_BF16, G9_BF16, G9_SCHED_DP, 4, g9_a16w16_bf16_moe_4w, "g9_a16w16_bf16_moe_4w"},
+    {G9_FP4, G9_BF16, G9_SCHED_DP, 4, g9_a4w4_bf16out_moe_4w, "g9_a4w4_bf16out_moe_4w"},
+    {G9_FP4, G9_F16, G9_SCHED_DP, 4, g9_a4w4_f16out_moe_4w, "g9_a4w4_f16out_moe_4w"},
+};
+
+const KernelEntry* find_moe_kernel(int dtype, int out) {
+  for (const KernelEntry& k : kMoeKernels)
+    if (k.dtype == dtype && k.out == out) return &k;
+  return nullptr;
+}
 
 const KernelEntry* find_kernel(int dtype, int out, int sched, int waves) {
   for (const KernelEntry& k : kKernels)
@@ -141,6 +165,41 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
   return hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3(grid), dim3(64 * waves), args, 0, s) == hipSuccess
              ? G9_OK
              : G9_ERR_HIP;
+}
+
+int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
+                 const void* c);
+
+// Shared launch path of the grouped kernels: T token rows, E experts.
+int launch_moe(int dtype, int out, GemmParams& p, int64_t E, void* stream) {
+  const KernelEntry* k = find_moe_kernel(dtype, out);
+  if (!k) return G9_ERR_DTYPE;
+  if (p.M == 0) return G9_OK;  // no tokens: nothing to write
+  // Upper bound of the experts' m-tiles: sum ceil(M_e / 256) <= ceil(T / 256) + E.
+  const long long tiles_m = (p.M + kTile - 1) / kTile + E;
+  p.tiles_n = (p.N + kTile - 1) / kTile;
+  if (tiles_m * p.tiles_n > INT32_MAX) return G9_ERR_SHAPE;
+  p.tiles_m = (int)tiles_m;
+  p.num_xcds = kNumXcds;
+  p.group_m = kGroupM;
+  p.moe_experts = (int)E;
+  void* args[] = {&p};
+  return hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3((unsigned)(tiles_m * p.tiles_n)), dim3(256),
+                         args, 0, reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}
+
+int check_moe(int64_t T, int64_t N, int64_t K, int64_t E, int dtype, int64_t stride_cm, const void* c,
+              const int32_t* offsets, int64_t stride_be) {
+  if (T < 0 || T > (1 << 30) || E <= 0 || E > (1 << 20)) return G9_ERR_SHAPE;
+  if (!offsets || !aligned(offsets, 4)) return G9_ERR_LAYOUT;
+  if (stride_be < 0 || stride_be % 16 != 0) return G9_ERR_LAYOUT;
+  if (T == 0) {  // only the remaining arguments' own validity matters
+    if (N <= 0 || K <= 0 || K % stage_k(dtype) != 0) return G9_ERR_SHAPE;
+    return G9_OK;
+  }
+  return check_common(T, N, K, dtype, stride_cm, 1, c);
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
@@ -248,6 +307,69 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(G9_FP4));
   return launch(G9_FP4, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+}
+
+int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_offsets, int64_t T,
+                  int64_t N, int64_t K, int64_t E, int64_t stride_am, int64_t stride_bn, int64_t stride_be,
+                  int64_t stride_cm, int dtype, void* stream) {
+  if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_moe(T, N, K, E, dtype, stride_cm, c, expert_offsets, stride_be);
+  if (st || T == 0) return st;
+  if ((st = check_operand(a, stride_am * 2, 1, K * 2))) return st;
+  if ((st = check_operand(b, stride_bn * 2, 1, K * 2))) return st;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.M = (int)T;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)(stride_am * 2);
+  p.ldb = (u32)(stride_bn * 2);
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(dtype));
+  p.moe_off = expert_offsets;
+  p.moe_b_stride = stride_be;
+  return launch_moe(dtype, dtype, p, E, stream);
+}
+
+int g9_moe_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                const int32_t* expert_offsets, int64_t T, int64_t N, int64_t K, int64_t E, int64_t stride_am,
+                int64_t stride_bn, int64_t stride_be, int64_t stride_asm, int64_t stride_bsn,
+                int64_t stride_bse, int64_t stride_cm, int out_dtype, void* stream) {
+  if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_moe(T, N, K, E, G9_FP4, stride_cm, c, expert_offsets, stride_be);
+  if (st || T == 0) return st;
+  if ((st = check_operand(a, stride_am, 1, K / 2))) return st;
+  if ((st = check_operand(b, stride_bn, 1, K / 2))) return st;
+  if (!a_scales || !b_scales || !aligned(a_scales, 4) || !aligned(b_scales, 4)) return G9_ERR_LAYOUT;
+  if (stride_asm % 4 || stride_bsn % 4 || stride_asm < K / 32 || stride_bsn < K / 32) return G9_ERR_LAYOUT;
+  if (stride_asm > (1 << 24) || stride_bsn > (1 << 24)) return G9_ERR_LAYOUT;
+  if (stride_bse < 0 || stride_bse % 4) return G9_ERR_LAYOUT;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.a_sc = static_cast<const unsigned char*>(a_scales);
+  p.b_sc = static_cast<const unsigned char*>(b_scales);
+  p.M = (int)T;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)stride_am;
+  p.ldb = (u32)stride_bn;
+  p.ldsa = (u32)stride_asm;
+  p.ldsb = (u32)stride_bsn;
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(G9_FP4));
+  p.moe_off = expert_offsets;
+  p.moe_b_stride = stride_be;
+  p.moe_bsc_stride = stride_bse;
+  return launch_moe(G9_FP4, out_dtype, p, E, stream);
+}
+
+const char* g9_moe_kernel_name(int dtype, int out_dtype) {
+  const KernelEntry* k = find_moe_kernel(dtype, out_dtype);
+  return k ? k->name : nullptr;
 }
 
 size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves) {

@@ -132,6 +132,12 @@ struct GemmParams {
   u32 epoch;
   int* err;                   // set to 1 when a flag wait times out
   int sk_ctas;                // persistent workgroups
+  // grouped (MoE) GEMM: expert e owns rows [moe_off[e], moe_off[e+1]) of A
+  // and C and its own B (and FP4 B scales) moe_b_stride (moe_bsc_stride)
+  // bytes after expert e - 1's
+  const int* moe_off;
+  int moe_experts;
+  long long moe_b_stride, moe_bsc_stride;
 };
 
 constexpr int kTile = 256;
@@ -920,6 +926,75 @@ G9_DEV void gemm_dp(const GemmParams& p) {
   timing_stamp(2);
   store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
   timing_stamp(3);
+}
+
+// Grouped ("MoE") GEMM over E experts: expert e multiplies rows
+// [off[e], off[e+1]) of A (tokens sorted by expert) by its own B_e into the
+// same rows of C.  The grid covers tiles_m x tiles_n tiles with tiles_m an
+// upper bound of the experts' m-tiles (sum of ceil(M_e / 256) <= ceil(M / 256)
+// + E); each workgroup finds the expert of its m-tile and then runs the
+// data-parallel tile unchanged on that expert's rows and weights.  Workgroups
+// past the last expert's tiles exit.  Offsets are clamped to [0, M] (and each
+// expert's end to at least its start), so any offset table keeps every access
+// inside A, C and the experts' B.
+
+// Expert of m-tile `mt`: 64 experts per pass, one per lane (their m-tile
+// counts, an inclusive wave prefix sum, a ballot for the lane whose range
+// holds mt).  Returns false if mt is past the last expert's tiles.
+G9_DEV bool moe_find(const GemmParams& p, int mt, int& expert, int& local_mt, int& row0, int& rows) {
+  const int lane = threadIdx.x & 63;
+  const int T = p.M;
+  int base = 0;
+  for (int e0 = 0; e0 < p.moe_experts; e0 += 64) {
+    const int e = e0 + lane;
+    int lo = 0, hi = 0, n = 0;
+    if (e < p.moe_experts) {
+      lo = min(max(p.moe_off[e], 0), T);
+      hi = min(max(p.moe_off[e + 1], lo), T);
+      n = (hi - lo + kTile - 1) / kTile;
+    }
+    int incl = n;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    const int first = base + incl - n;
+    const unsigned long long hit = __ballot(n > 0 && mt >= first && mt < base + incl);
+    if (hit) {
+      const int l = __ffsll((long long)hit) - 1;
+      expert = __builtin_amdgcn_readfirstlane(__shfl(e, l, 64));
+      local_mt = __builtin_amdgcn_readfirstlane(mt - __shfl(first, l, 64));
+      row0 = __builtin_amdgcn_readfirstlane(__shfl(lo, l, 64));
+      rows = __builtin_amdgcn_readfirstlane(__shfl(hi - lo, l, 64));
+      return true;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  return false;
+}
+
+template <Op OP, int OUT, class G>
+G9_DEV void gemm_moe(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes<OpInfo<OP>::kScaled>];
+  int mt, tn;
+  tile_coords(blockIdx.x, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, p.num_xcds, p.group_m, mt, tn);
+  int expert, tm, row0, rows;
+  if (!moe_find(p, mt, expert, tm, row0, rows)) return;
+  GemmParams q = p;
+  q.a = p.a + (size_t)row0 * p.lda;
+  q.c = p.c + (size_t)row0 * p.ldc * 2;
+  q.b = p.b + (size_t)expert * p.moe_b_stride;
+  q.M = rows;
+  if constexpr (OpInfo<OP>::kScaled) {
+    q.a_sc = p.a_sc + (size_t)row0 * p.ldsa;
+    q.b_sc = p.b_sc + (size_t)expert * p.moe_bsc_stride;
+  }
+  Acc<G> acc;
+  zero_acc<G>(acc);
+  pin_acc<G>(acc);
+  mainloop<OP, G>(q, smem, tm, tn, 0, q.ns, acc, false);
+  store_tile<OUT, G>(q, smem, tm, tn, acc, epilogue_scale<OP>(q));
 }
 
 // ---------------------------------------------------------------------------

@@ -91,6 +91,38 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
                  void* stream);
 
 /*
+ * Grouped ("MoE") GEMMs over E experts, 4-wave, data-parallel tiles.  The
+ * rows of A (tokens, T in total) are sorted by expert: expert e owns rows
+ * [expert_offsets[e], expert_offsets[e+1]) of A and of C and multiplies them
+ * by its own B_e, the N x K operand stride_be bytes after B_(e-1) (rows
+ * stride_bn apart, K-contiguous).  expert_offsets is a device array of E + 1
+ * int32 prefix sums (offsets[0] = 0, offsets[E] <= T); rows of C outside every
+ * expert's range are not written, offsets are clamped to [0, T] (so no table
+ * makes the kernel access memory outside A, C and the E experts' B), and an
+ * expert with no rows costs nothing.  No counterpart in the reference: its
+ * roadmap plans an MXFP4 MoE kernel (its ROADMAP.md, "4-bit + Scales").
+ *
+ * g9_moe_a16w16: FP16 / BF16 (`dtype`), strides in elements except stride_be
+ * (bytes); K a multiple of 64.
+ */
+int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_offsets, int64_t T,
+                  int64_t N, int64_t K, int64_t E, int64_t stride_am, int64_t stride_bn, int64_t stride_be,
+                  int64_t stride_cm, int dtype, void* stream);
+
+/*
+ * g9_moe_a4w4: MXFP4 as g9_gemm_a4w4 (strides in bytes); expert e's weights are
+ * b + e * stride_be (N x K/2 bytes) and its scales b_scales + e * stride_bse
+ * (N x K/32 bytes); `out_dtype` G9_BF16 or G9_F16.  K a multiple of 256.
+ */
+int g9_moe_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                const int32_t* expert_offsets, int64_t T, int64_t N, int64_t K, int64_t E, int64_t stride_am,
+                int64_t stride_bn, int64_t stride_be, int64_t stride_asm, int64_t stride_bsn,
+                int64_t stride_bse, int64_t stride_cm, int out_dtype, void* stream);
+
+/* Name of the grouped kernel g9_moe_* launches for (dtype, out_dtype), or NULL. */
+const char* g9_moe_kernel_name(int dtype, int out_dtype);
+
+/*
  * Bytes of stream-K workspace a call with these arguments needs (0 for the
  * data-parallel schedule).  `dtype` is the operand type.
  * No counterpart in the reference (it has no stream-K schedule).

@@ -14,8 +14,8 @@ It restates, in numpy, the reference's correctness path for this GEMM:
 * a4w4: ``torch_reference`` = fp32 mm of the dequantized MXFP4 operands, cast
   to bf16 (kernels/gemm/intra_wave/a4w4/bench.py:77-164);
 * the data-parallel tile map ``get_pids`` (kernels/gemm/utils/common.py:38-83);
-* the per-tensor e5m2 and OCP-MX MXFP4 quantizers and the stream-K work
-  partition, which have no counterpart in the reference (they are defined by
+* the per-tensor e5m2 and OCP-MX MXFP4 quantizers, the stream-K work
+  partition and the grouped (MoE) GEMM, which have no counterpart in the reference (they are defined by
   the BASELINE configurations and the OCP Microscaling Formats v1.0 spec).
 
 How each function is pinned (golden fixtures made with exact rational
@@ -223,6 +223,27 @@ def a4w4_ref(a: np.ndarray, b: np.ndarray, a_scales: np.ndarray, b_scales: np.nd
 
 def a4w4_ref_f32(a, b, a_scales, b_scales) -> np.ndarray:
     return gemm_f32(mxfp4_dequant(a, a_scales), mxfp4_dequant(b, b_scales))
+
+
+def moe_ref(dense, a_rows, b_experts, offsets, *row_args, expert_args=()):
+    """Grouped GEMM (no counterpart in the reference): expert e applies
+    ``dense`` to rows [offsets[e], offsets[e+1]) of each row operand (a_rows and
+    row_args, e.g. A's scales) and its own slice of each expert operand
+    (b_experts and expert_args, e.g. B's scales).  Rows no expert owns are NaN."""
+    offsets = np.asarray(offsets, dtype=np.int64)
+    E = len(offsets) - 1
+    out = None
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi <= lo:
+            continue
+        r = dense(a_rows[lo:hi], b_experts[e], *[x[lo:hi] for x in row_args], *[x[e] for x in expert_args])
+        if out is None:
+            out = np.full((a_rows.shape[0], r.shape[1]), np.nan, dtype=r.dtype)
+        out[lo:hi] = r
+    if out is None:
+        out = np.full((a_rows.shape[0], b_experts.shape[1]), np.nan, dtype=np.float32)
+    return out
 
 
 def rel_frobenius(x: np.ndarray, ref: np.ndarray) -> float:

@@ -240,3 +240,29 @@ def test_product_host_get_pids_matches_oracle(grid_m, grid_n):
     for pid in range(grid):
         args = (pid, grid_m * 256, grid_n * 256, 256, 256, grid, 8, 4)
         assert get_pids(*args) == R.get_pids(*args)
+
+
+def test_moe_ref_routes_rows_to_their_expert():
+    # A rows of ones; expert e's weights are the constant v_e, so row t of expert e is K * v_e exactly.
+    K = 64
+    a = np.ones((7, K), np.float16)
+    vals = (1.0, 2.0, 0.5, 4.0)
+    b = np.stack([np.full((3, K), v, np.float16) for v in vals])
+    offsets = [1, 3, 3, 6, 6]  # row 0 and row 6 belong to no expert; experts 1 and 3 are empty
+    c = R.moe_ref(R.a16w16_ref, a, b, offsets)
+    assert np.all(np.isnan(c[0])) and np.all(np.isnan(c[6]))
+    np.testing.assert_array_equal(c[1:3], np.full((2, 3), K * 1.0))
+    np.testing.assert_array_equal(c[3:6], np.full((3, 3), K * 0.5))
+
+
+def test_moe_ref_passes_row_and_expert_operands():
+    # MXFP4: A codes 2 (value 1.0) with scale 127 (1.0); expert e's B codes 2 with scale 127 + e, so
+    # row t of expert e is K * 2^e.
+    K, T, N = 64, 4, 2
+    a = R.pack_fp4(np.full((T, K), 2, np.uint8))
+    a_sc = np.full((T, K // 32), 127, np.uint8)
+    b = np.stack([R.pack_fp4(np.full((N, K), 2, np.uint8)) for _ in range(3)])
+    b_sc = np.stack([np.full((N, K // 32), 127 + e, np.uint8) for e in range(3)])
+    c = R.moe_ref(R.a4w4_ref_f32, a, b, [0, 1, 1, 4], a_sc, expert_args=(b_sc,))
+    np.testing.assert_array_equal(c[0], [K, K])
+    np.testing.assert_array_equal(c[1:], np.full((3, N), K * 4.0))
