@@ -60,6 +60,7 @@ def parse_args():
                    help="also time bf8 at K=16384 and mxfp4 at K=32768, the reference's headline shapes")
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
     p.add_argument("--waves", default="4,8", help="wave schedules to time: 4 (1 wave/SIMD), 8 (2 waves/SIMD)")
+    p.add_argument("--moe", type=int, default=1, help="also time the grouped (MoE) GEMMs (0/1)")
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--serialized", type=int, default=0,
@@ -369,6 +370,64 @@ def streamk_fixups(tiles: int, stages: int, ctas: int) -> int:
     return sum(1 for c in range(1, ctas) if (c * base + min(c, rem)) % stages)
 
 
+# Grouped (MoE) GEMM benchmark: 32 experts, 32768 routed tokens (1024 per expert
+# on average, Dirichlet(5)-skewed), N = 4096 (a fused gate/up projection), K = 7168.
+MOE_SHAPE = {"E": 32, "T": 32768, "N": 4096, "K": 7168}
+
+
+def moe_counts(E: int, T: int, seed: int = 7):
+    """Tokens per expert: a seeded multinomial draw from Dirichlet(5) shares."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return rng.multinomial(T, rng.dirichlet([5.0] * E))
+
+
+def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
+    """Returns (launch(i), counts): the grouped GEMM on operand set i.  The
+    operands are generated on the device (seeded) to keep set-up short."""
+    import numpy as np
+    import torch
+
+    from gfx950_gluon_tutorials_amd import quant
+    from gfx950_gluon_tutorials_amd.gemm.moe import moe_matmul, moe_matmul_a4w4
+
+    E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
+    counts = moe_counts(E, T)
+    off = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        a = torch.randn(T, K, generator=gen, device=dev)
+        if dtype == "fp16":
+            b = torch.randn(E, N, K, generator=gen, device=dev, dtype=torch.float16)
+            sets.append((a.half(), b, torch.empty(T, N, dtype=torch.float16, device=dev)))
+        else:
+            pa, sa = quant.quantize_mxfp4(a)
+            pb = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
+            sb = torch.empty(E, N, K // 32, dtype=torch.uint8, device=dev)
+            for e in range(E):
+                pb[e], sb[e] = quant.quantize_mxfp4(torch.randn(N, K, generator=gen, device=dev))
+            sets.append((pa, pb, sa, sb, torch.empty(T, N, dtype=torch.bfloat16, device=dev)))
+        del a
+
+    def launch(i, schedule="dp"):
+        x = sets[i % nsets]
+        if dtype == "fp16":
+            moe_matmul(x[0], x[1], off, x[2])
+        else:
+            moe_matmul_a4w4(x[0], x[1], x[2], x[3], off, x[4])
+
+    return launch, counts
+
+
+def moe_set_bytes(dtype: str) -> int:
+    E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
+    if dtype == "fp16":
+        return 2 * (T * K + E * N * K + T * N)
+    return (T * K + E * N * K) // 2 + (T + E * N) * K // 32 + 2 * T * N
+
+
 def load_traffic(key: str):
     try:
         with open(TRAFFIC_FILE) as f:
@@ -452,6 +511,25 @@ def main():
                   flush=True)
             del launch
             torch.cuda.empty_cache()
+    moe = {}
+    if args.moe and not args.only:
+        E, T, N, K_ = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
+        for dt in ("mxfp4", "fp16"):
+            nsets = max(2, -(-args.rotate_mb * 2**20 // moe_set_bytes(dt)))
+            launch, counts = make_moe_case(dt, dev, nsets)
+            ms = time_case(launch, max(20, args.steps // 4), args.warmup // 4, settle_s=args.settle_ms / 2e3)
+            flop = 2.0 * T * N * K_
+            padded = sum(-(-int(c) // 256) * 256 for c in counts)
+            tf = flop / (ms * 1e-3) / 1e12
+            moe[dt] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
+                       "experts": E, "tokens": T, "N": N, "K": K_, "rotating_sets": nsets,
+                       "min_max_tokens": [int(counts.min()), int(counts.max())],
+                       "row_utilization": round(T / padded, 4)}
+            print(f"# moe {dt}: E={E} T={T} N={N} K={K_} (tokens/expert {counts.min()}-{counts.max()}): "
+                  f"{ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak  "
+                  f"(256-row tiles {100 * T / padded:.1f}% filled)", flush=True)
+            del launch
+            torch.cuda.empty_cache()
     if args.copy_mb:
         copy_calibration(args.copy_mb, dev)
     head = "fp16" if "fp16" in results else next(iter(results))
@@ -477,6 +555,7 @@ def main():
                      "frac": r["frac_of_peak"], "traffic": load_traffic(f"{head}_{M}x{N}x{K}")},
         "per_dtype": results,
         "streamk": sk,
+        "moe": moe,
     }
     if args.cpu_baseline and not args.only:
         line["cpu_baseline"] = cpu_baseline(head.split("_")[0], M, N, K, seeds[head.split("_")[0]])
