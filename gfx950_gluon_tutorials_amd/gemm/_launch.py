@@ -26,30 +26,35 @@ _OUT_CODE = {torch.float16: _lib.G9_F16, torch.bfloat16: _lib.G9_BF16}
 STAGE_K = {_lib.G9_F16: 64, _lib.G9_BF16: 64, _lib.G9_BF8: 128, _lib.G9_FP4: 256}
 
 
-# schedule="auto": stream-K where it measured faster than data-parallel (fp16,
-# 4-wave, one MI355X at steady state): more 256x256 tiles than CUs but at most
-# 1.25 waves of them (272 tiles: +27%, 320: +8%).  Data-parallel otherwise:
-# with fewer tiles than CUs the K-ordered stream-K chains cannot shorten a tile
-# (3840^2: -11%), and from ~1.3 waves the workgroups' misaligned K offsets cost
-# more L2 traffic than the balance gains (324 tiles: +2%, 400 tiles: -18%).
+# schedule="auto": stream-K where it measured faster than data-parallel (one
+# MI355X at steady state, K = 8192): FP16/BF16 outputs of more 256x256 tiles
+# than CUs but at most 1.25 waves of them (272 tiles: +25% 4-wave, +13%
+# 8-wave; 320 tiles: +9% / +1%).  Data-parallel otherwise: with fewer tiles
+# than CUs the K-ordered stream-K chains cannot shorten a tile (3840^2: -11%),
+# from ~1.3 waves the workgroups' misaligned K offsets cost more L2 traffic
+# than the balance gains (400 tiles: -18%), and BF8 and MXFP4, with 2-4x
+# fewer K stages per tile to amortise a partial-tile handoff, lose at 272
+# tiles already (BF8 -2%, MXFP4 -21%).
 AUTO_SK_MAX_WAVES = 1.25
 
 
-def auto_schedule(M: int, N: int, cus: int | None = None) -> int:
-    """The schedule code schedule="auto" picks for an M x N output on a device
-    with `cus` compute units (queried when None)."""
+def auto_schedule(M: int, N: int, cus: int | None = None, dtype: int = _lib.G9_F16) -> int:
+    """The schedule code schedule="auto" picks for an M x N output of operand
+    type `dtype` on a device with `cus` compute units (queried when None)."""
+    if dtype not in (_lib.G9_F16, _lib.G9_BF16):
+        return _lib.G9_SCHED_DP
     tiles = -(-M // 256) * -(-N // 256)
     if cus is None:
         cus = _lib.load().g9_streamk_workgroups()
     return _lib.G9_SCHED_SK if 0 < cus < tiles <= AUTO_SK_MAX_WAVES * cus else _lib.G9_SCHED_DP
 
 
-def _schedule_code(schedule, M: int, N: int) -> int:
+def _schedule_code(schedule, M: int, N: int, dtype: int) -> int:
     if isinstance(schedule, int):
         return schedule
     name = str(schedule).lower()
     if name == "auto":
-        return auto_schedule(M, N)
+        return auto_schedule(M, N, dtype=dtype)
     try:
         return _lib.SCHEDULES[name]
     except KeyError:
@@ -145,7 +150,7 @@ def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedul
         a = a.contiguous()
     b_kn = _k_major(b_kn)
     dt = _DTYPE_CODE[a.dtype]
-    sched = _schedule_code(schedule, M, N)
+    sched = _schedule_code(schedule, M, N, dt)
     stream = _stream(dev)
     ws, ws_bytes = _workspace(lib, dt, M, N, K, sched, waves, dev, stream)
     rc = lib.g9_gemm_a16w16(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
@@ -183,7 +188,7 @@ def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=N
     b_kn = _k_major(b_kn)
     sa = _scale_tensor(a_scale, dev)
     sb = _scale_tensor(b_scale, dev)
-    sched = _schedule_code(schedule, M, N)
+    sched = _schedule_code(schedule, M, N, _lib.G9_BF8)
     stream = _stream(dev)
     ws, ws_bytes = _workspace(lib, _lib.G9_BF8, M, N, K, sched, waves, dev, stream)
     rc = lib.g9_gemm_a8w8(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
@@ -229,7 +234,7 @@ def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales
         a_scales = a_scales.contiguous()
     if not _scales_ok(b_scales):
         b_scales = b_scales.contiguous()
-    sched = _schedule_code(schedule, M, N)
+    sched = _schedule_code(schedule, M, N, _lib.G9_FP4)
     stream = _stream(dev)
     ws, ws_bytes = _workspace(lib, _lib.G9_FP4, M, N, K, sched, waves, dev, stream)
     rc = lib.g9_gemm_a4w4(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(),

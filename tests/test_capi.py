@@ -138,3 +138,6 @@ def test_auto_schedule_rule():
     for (M, N), want in cases.items():
         assert _launch.auto_schedule(M, N, cus=256) == want, (M, N)
     assert _launch.auto_schedule(4352, 4096, cus=0) == dp  # no device: never stream-K
+    assert _launch.auto_schedule(4352, 4096, cus=256, dtype=_lib.G9_BF16) == sk
+    for dt in (_lib.G9_BF8, _lib.G9_FP4):  # fewer K stages per tile: stream-K measured slower
+        assert _launch.auto_schedule(4352, 4096, cus=256, dtype=dt) == dp
