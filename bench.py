@@ -61,6 +61,9 @@ def parse_args():
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
     p.add_argument("--waves", default="4,8", help="wave schedules to time: 4 (1 wave/SIMD), 8 (2 waves/SIMD)")
     p.add_argument("--moe", type=int, default=1, help="also time the grouped (MoE) GEMMs (0/1)")
+    p.add_argument("--vendor", type=int, default=1,
+                   help="also time ROCm's hipBLASLt (torch.matmul / torch._scaled_mm) on the same shapes, "
+                        "interleaved with ours, for fp16/bf16/bf8 at K=8192 (0/1)")
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--serialized", type=int, default=0,
@@ -421,6 +424,39 @@ def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
     return launch, counts
 
 
+def make_vendor_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
+    """launch(i) running ROCm's library GEMM (hipBLASLt through torch) on the
+    same kind of operands as make_case: torch.matmul for fp16/bf16,
+    torch._scaled_mm (e5m2 x e5m2 -> bf16, per-tensor scales) for bf8."""
+    import torch
+
+    from gfx950_gluon_tutorials_amd import quant
+
+    gen = torch.Generator().manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        if dtype in ("fp16", "bf16"):
+            tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+            a = (torch.randn(M, K, generator=gen) * 0.1).to(tdt).to(dev)
+            b = (torch.randn(N, K, generator=gen) * 0.1).to(tdt).to(dev)
+            sets.append((a, b, torch.empty(M, N, dtype=tdt, device=dev)))
+        else:
+            qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=gen).to(dev))
+            qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=gen).to(dev))
+            sets.append((qa, qb, sa.reshape(()).float(), sb.reshape(()).float()))
+
+    def launch(i, schedule="dp"):
+        x = sets[i % nsets]
+        if dtype in ("fp16", "bf16"):
+            torch.matmul(x[0], x[1].T, out=x[2])
+        else:
+            torch._scaled_mm(x[0], x[1].T, scale_a=x[2], scale_b=x[3], out_dtype=torch.bfloat16)
+
+    launch(0)  # raises here if the library has no kernel for this case
+    torch.cuda.synchronize()
+    return launch
+
+
 def moe_set_bytes(dtype: str) -> int:
     E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
     if dtype == "fp16":
@@ -488,6 +524,25 @@ def main():
                 print(f"#   steady state {tel['launch_us']:.1f} us ({tel['tflops']:.0f} TFLOPS) at "
                       f"{tel['power_w']:.0f} W, GFX clock {tel['gfx_clock_mhz']} MHz (amd-smi, {tel['samples']} samples)",
                       flush=True)
+        if args.vendor and not args.only and kk == K and w == 4 and dt in ("fp16", "bf16", "bf8"):
+            try:
+                vlaunch = make_vendor_case(dt, M, N, kk, seeds[dt], dev, nsets)
+            except Exception as e:  # no library kernel for this type on this build
+                results[key]["vendor"] = {"library": "hipBLASLt via torch", "error": str(e).splitlines()[0][:120]}
+            else:
+                # interleaved, three rounds each, so board drift hits both equally
+                t_ours, t_lib = [], []
+                for _ in range(3):
+                    t_ours.append(time_case(launch, max(20, args.steps // 2), 20, settle_s=0.3))
+                    t_lib.append(time_case(vlaunch, max(20, args.steps // 2), 20, settle_s=0.3))
+                mo, ml = sorted(t_ours)[1], sorted(t_lib)[1]
+                tf_o, tf_l = 2.0 * M * N * kk / (mo * 1e-3) / 1e12, 2.0 * M * N * kk / (ml * 1e-3) / 1e12
+                results[key]["vendor"] = {"library": "hipBLASLt via torch." + ("matmul" if dt != "bf8" else "_scaled_mm"),
+                                          "tflops": round(tf_l, 2), "ours_interleaved_tflops": round(tf_o, 2),
+                                          "ours_over_library": round(tf_o / tf_l, 4)}
+                print(f"#   same box, interleaved: ours {tf_o:.1f} vs hipBLASLt {tf_l:.1f} TFLOPS ({tf_o / tf_l:.3f}x)",
+                      flush=True)
+                del vlaunch
         del launch
         torch.cuda.empty_cache()
     sk = {}
