@@ -74,6 +74,9 @@ def parse_args():
     p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
     p.add_argument("--telemetry-s", type=float, default=3.0,
                    help="run the headline case this long while sampling board power and clock (0: skip)")
+    p.add_argument("--pair", type=int, default=0,
+                   help="profiler target: run our 4-wave kernel and hipBLASLt on the --only dtype (fp16 by "
+                        "default) N times each at 4096x4096x8192, then exit")
     p.add_argument("--summarize", default="",
                    help="print a per-kernel summary of the rocprofv3 SQLite output under this directory and exit")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -486,6 +489,18 @@ def main():
     dev = torch.device("cuda:0")
     M = N = 4096
     K = 8192
+    if args.pair:
+        dt = args.only or "fp16"
+        seed = {"fp16": 1, "bf16": 1, "bf8": 2}[dt]
+        ours, lib = make_case(dt, M, N, K, seed, dev, 4, 4), make_vendor_case(dt, M, N, K, seed, dev, 4)
+        for i in range(args.pair):
+            ours(i, "dp")
+        torch.cuda.synchronize()
+        for i in range(args.pair):
+            lib(i)
+        torch.cuda.synchronize()
+        print(f"# pair: {args.pair} launches each of ours and hipBLASLt ({dt})", flush=True)
+        return
     dtypes = [d for d in args.dtypes.split(",") if d]
     if args.only:
         dtypes = [args.only]
