@@ -105,3 +105,27 @@ def test_moe_clamps_out_of_range_offsets(gpu):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(_bits(c[:100]), _bits(a16w16_matmul(a[:100].contiguous(), b[0].T)))
     np.testing.assert_array_equal(_bits(c[250:]), _bits(a16w16_matmul(a[100:].contiguous(), b[2].T)[150:]))
+
+
+def test_moe_many_experts_multi_pass_lookup(gpu):
+    # 130 experts: the lookup walks the offsets 64 experts per pass (three passes); most experts are small
+    # or empty, a few span several m-tiles.
+    _say("moe a16w16 130 experts")
+    rng = np.random.default_rng(15)
+    E, N, K = 130, 256, 128
+    counts = rng.integers(0, 40, E)
+    counts[rng.random(E) < 0.3] = 0
+    counts[[5, 70, 129]] = [300, 513, 257]
+    T = int(counts.sum())
+    g = torch.Generator().manual_seed(15)
+    a = (torch.randn(T, K, generator=g) * 0.1).half().to(gpu)
+    b = (torch.randn(E, N, K, generator=g) * 0.1).half().to(gpu)
+    off = _offsets(counts, gpu)
+    c = moe_matmul(a, b, off)
+    torch.cuda.synchronize()
+    o = off.cpu().numpy()
+    ref = R.moe_ref(R.a16w16_ref, a.cpu().numpy(), b.cpu().numpy(), o)
+    assert np.allclose(c.float().cpu().numpy(), ref, rtol=1e-2, atol=1e-2 * np.sqrt(K) * 0.01)
+    for e in (5, 70, 129):
+        lo, hi = int(o[e]), int(o[e + 1])
+        np.testing.assert_array_equal(_bits(c[lo:hi]), _bits(a16w16_matmul(a[lo:hi].contiguous(), b[e].T)))
