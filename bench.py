@@ -396,7 +396,7 @@ def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
     import torch
 
     from gfx950_gluon_tutorials_amd import quant
-    from gfx950_gluon_tutorials_amd.gemm.moe import moe_matmul, moe_matmul_a4w4
+    from gfx950_gluon_tutorials_amd.gemm.moe import moe_matmul, moe_matmul_a4w4, moe_matmul_a8w8
 
     E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
     counts = moe_counts(E, T)
@@ -408,6 +408,13 @@ def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
         if dtype == "fp16":
             b = torch.randn(E, N, K, generator=gen, device=dev, dtype=torch.float16)
             sets.append((a.half(), b, torch.empty(T, N, dtype=torch.float16, device=dev)))
+        elif dtype == "bf8":
+            qa, sa = quant.quantize_e5m2(a)
+            qb = torch.empty(E, N, K, dtype=torch.float8_e5m2, device=dev)
+            sb = torch.empty(E, dtype=torch.float32, device=dev)
+            for e in range(E):
+                qb[e], sb[e] = quant.quantize_e5m2(torch.randn(N, K, generator=gen, device=dev))
+            sets.append((qa, qb, sa, sb, torch.empty(T, N, dtype=torch.bfloat16, device=dev)))
         else:
             pa, sa = quant.quantize_mxfp4(a)
             pb = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
@@ -421,6 +428,8 @@ def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
         x = sets[i % nsets]
         if dtype == "fp16":
             moe_matmul(x[0], x[1], off, x[2])
+        elif dtype == "bf8":
+            moe_matmul_a8w8(x[0], x[1], off, x[4], a_scale=x[2], b_scales=x[3])
         else:
             moe_matmul_a4w4(x[0], x[1], x[2], x[3], off, x[4])
 
@@ -464,6 +473,8 @@ def moe_set_bytes(dtype: str) -> int:
     E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
     if dtype == "fp16":
         return 2 * (T * K + E * N * K + T * N)
+    if dtype == "bf8":
+        return T * K + E * N * K + 2 * T * N
     return (T * K + E * N * K) // 2 + (T + E * N) * K // 32 + 2 * T * N
 
 
@@ -584,7 +595,7 @@ def main():
     moe = {}
     if args.moe and not args.only:
         E, T, N, K_ = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
-        for dt in ("mxfp4", "fp16"):
+        for dt in ("mxfp4", "bf8", "fp16"):
             nsets = max(2, -(-args.rotate_mb * 2**20 // moe_set_bytes(dt)))
             launch, counts = make_moe_case(dt, dev, nsets)
             ms = time_case(launch, max(20, args.steps // 4), args.warmup // 4, settle_s=args.settle_ms / 2e3)

@@ -52,6 +52,8 @@ SIGNATURES = {
     "g9_gemm_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]),
     "g9_moe_a16w16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "g9_moe_a8w8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                           _vp]),
     "g9_moe_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i64, _int, _vp]),
     "g9_moe_kernel_name": (ctypes.c_char_p, [_int, _int]),

@@ -44,6 +44,8 @@ G9_DEFINE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
 G9_DEFINE_MOE(g9_a16w16_f16, Op::F16, OUT_F16)
 G9_DEFINE_MOE(g9_a16w16_bf16, Op::BF16, OUT_BF16)
+G9_DEFINE_MOE(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
+G9_DEFINE_MOE(g9_a8w8_f16out, Op::BF8, OUT_F16)
 G9_DEFINE_MOE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
 G9_DEFINE_MOE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
@@ -73,6 +75,8 @@ const KernelEntry kKernels[] = {
 const KernelEntry kMoeKernels[] = {
     {G9_F16, G9_F16, G9_SCHED_DP, 4, g9_a16w16_f16_moe_4w, "g9_a16w16_f16_moe_4w"},
     {G9_BF16, G9_BF16, G9_SCHED_DP, 4, g9_a16w16_bf16_moe_4w, "g9_a16w16_bf16_moe_4w"},
+    {G9_BF8, G9_BF16, G9_SCHED_DP, 4, g9_a8w8_bf16out_moe_4w, "g9_a8w8_bf16out_moe_4w"},
+    {G9_BF8, G9_F16, G9_SCHED_DP, 4, g9_a8w8_f16out_moe_4w, "g9_a8w8_f16out_moe_4w"},
     {G9_FP4, G9_BF16, G9_SCHED_DP, 4, g9_a4w4_bf16out_moe_4w, "g9_a4w4_bf16out_moe_4w"},
     {G9_FP4, G9_F16, G9_SCHED_DP, 4, g9_a4w4_f16out_moe_4w, "g9_a4w4_f16out_moe_4w"},
 };
@@ -331,6 +335,33 @@ int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_o
   p.moe_off = expert_offsets;
   p.moe_b_stride = stride_be;
   return launch_moe(dtype, dtype, p, E, stream);
+}
+
+int g9_moe_a8w8(const void* a, const void* b, void* c, const int32_t* expert_offsets, const float* a_scale,
+                const float* b_scales, int64_t T, int64_t N, int64_t K, int64_t E, int64_t stride_am,
+                int64_t stride_bn, int64_t stride_be, int64_t stride_cm, int out_dtype, void* stream) {
+  if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_moe(T, N, K, E, G9_BF8, stride_cm, c, expert_offsets, stride_be);
+  if (st || T == 0) return st;
+  if ((st = check_operand(a, stride_am, 1, K))) return st;
+  if ((st = check_operand(b, stride_bn, 1, K))) return st;
+  if ((a_scale && !aligned(a_scale, 4)) || (b_scales && !aligned(b_scales, 4))) return G9_ERR_LAYOUT;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.a_scale = a_scale;
+  p.b_scale = b_scales;
+  p.M = (int)T;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)stride_am;
+  p.ldb = (u32)stride_bn;
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(G9_BF8));
+  p.moe_off = expert_offsets;
+  p.moe_b_stride = stride_be;
+  return launch_moe(G9_BF8, out_dtype, p, E, stream);
 }
 
 int g9_moe_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,

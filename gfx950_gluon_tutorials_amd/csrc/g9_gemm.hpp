@@ -929,8 +929,8 @@ G9_DEV void gemm_dp(const GemmParams& p) {
 }
 
 // Grouped ("MoE") GEMM over E experts: expert e multiplies rows
-// [off[e], off[e+1]) of A (tokens sorted by expert) by its own B_e into the
-// same rows of C.  The grid covers tiles_m x tiles_n tiles with tiles_m an
+// [off[e], off[e+1]) of A (tokens sorted by expert) by its own B_e (for BF8
+// with its own fp32 scale b_scale[e]) into the same rows of C.  The grid covers tiles_m x tiles_n tiles with tiles_m an
 // upper bound of the experts' m-tiles (sum of ceil(M_e / 256) <= ceil(M / 256)
 // + E); each workgroup finds the expert of its m-tile and then runs the
 // data-parallel tile unchanged on that expert's rows and weights.  Workgroups
@@ -989,6 +989,10 @@ G9_DEV void gemm_moe(const GemmParams& p) {
   if constexpr (OpInfo<OP>::kScaled) {
     q.a_sc = p.a_sc + (size_t)row0 * p.ldsa;
     q.b_sc = p.b_sc + (size_t)expert * p.moe_bsc_stride;
+  }
+  if constexpr (OP == Op::BF8) {
+    // BF8: one fp32 scale per expert for B (b_scale[expert]); A's is per tensor.
+    if (p.b_scale) q.b_scale = p.b_scale + expert;
   }
   Acc<G> acc;
   zero_acc<G>(acc);

@@ -4,10 +4,10 @@ No counterpart in the reference: its roadmap plans an MXFP4 MoE kernel
 ("4-bit + Scales" in its ROADMAP.md).  The operands follow the dense wrappers'
 layouts, with an expert dimension in front of B:
 
-* ``a``: (T, K) tokens (fp16/bf16), or (T, K/2) packed MXFP4 bytes, rows
-  sorted by expert;
+* ``a``: (T, K) tokens (fp16/bf16 or BF8 e5m2), or (T, K/2) packed MXFP4
+  bytes, rows sorted by expert;
 * ``b``: (E, N, K) expert weights, or (E, N, K/2) packed MXFP4 bytes, each
-  expert's N rows K-contiguous;
+  expert's N rows K-contiguous; BF8 takes one fp32 scale per expert;
 * ``a_scales`` (T, K/32) and ``b_scales`` (E, N, K/32) E8M0 bytes for MXFP4;
 * ``expert_offsets``: (E + 1,) int32 on the device, prefix sums of the tokens
   per expert (offsets[0] = 0, offsets[E] <= T): expert e owns rows
@@ -64,6 +64,44 @@ def moe_matmul(a: torch.Tensor, b: torch.Tensor, expert_offsets: torch.Tensor, c
                                    a.stride(0), b.stride(1), b.stride(0) * es, c.stride(0), _DTYPE_CODE[a.dtype],
                                    _stream(dev))
     _lib.check(rc, "g9_moe_a16w16")
+    return c
+
+
+def moe_matmul_a8w8(a: torch.Tensor, b: torch.Tensor, expert_offsets: torch.Tensor, c: torch.Tensor | None = None,
+                    *, a_scale=None, b_scales=None, out_dtype=torch.bfloat16):
+    """BF8 (fp8 e5m2) grouped GEMM: a (T, K), b (E, N, K); C rows of expert e =
+    (A . B_e^T) * a_scale * b_scales[e] in out_dtype.  a_scale: one fp32 value
+    (tensor or float), b_scales: E fp32 values; None = 1."""
+    assert a.dim() == 2 and b.dim() == 3 and a.shape[1] == b.shape[2], "Incompatible dimensions"
+    T, K = a.shape
+    E, N = b.shape[0], b.shape[1]
+    if c is None:
+        c = torch.empty((T, N), device=a.device, dtype=out_dtype)
+    dev = _require_device(a, b, c)
+    if a.dtype != torch.float8_e5m2 or b.dtype != torch.float8_e5m2:
+        raise ValueError(f"moe a8w8 needs float8_e5m2 operands; got {a.dtype}, {b.dtype}")
+    if c.dtype not in _OUT_CODE:
+        raise ValueError(f"moe a8w8 output must be bf16 or fp16, got {c.dtype}")
+    if c.shape != (T, N) or c.stride(1) != 1:
+        raise ValueError(f"c must be a ({T}, {N}) row-major view, got {tuple(c.shape)} strides {c.stride()}")
+    off = _offsets(expert_offsets, dev, E)
+    a, b = _rows(a), _rows(b)
+    sa = None
+    if a_scale is not None:
+        sa = a_scale if isinstance(a_scale, torch.Tensor) else torch.tensor([float(a_scale)])
+        if sa.numel() != 1:
+            raise ValueError("a_scale is per tensor: one fp32 value")
+        sa = sa.detach().reshape(1).to(device=dev, dtype=torch.float32)
+    sb = None
+    if b_scales is not None:
+        if not isinstance(b_scales, torch.Tensor) or b_scales.numel() != E:
+            raise ValueError(f"b_scales must be a tensor of E = {E} fp32 values")
+        sb = b_scales.detach().reshape(E).to(device=dev, dtype=torch.float32).contiguous()
+    rc = _lib.load().g9_moe_a8w8(a.data_ptr(), b.data_ptr(), c.data_ptr(), off.data_ptr(),
+                                 sa.data_ptr() if sa is not None else None, sb.data_ptr() if sb is not None else None,
+                                 T, N, K, E, a.stride(0), b.stride(1), b.stride(0), c.stride(0), _OUT_CODE[c.dtype],
+                                 _stream(dev))
+    _lib.check(rc, "g9_moe_a8w8")
     return c
 
 

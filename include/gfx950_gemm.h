@@ -110,6 +110,16 @@ int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_o
                   int64_t stride_cm, int dtype, void* stream);
 
 /*
+ * g9_moe_a8w8: BF8 (fp8 e5m2) as g9_gemm_a8w8 (strides in bytes): C rows of
+ * expert e = (A . B_e^T) * a_scale[0] * b_scales[e], with a_scale one device
+ * fp32 value and b_scales E of them (either NULL = 1.0); `out_dtype` G9_BF16
+ * or G9_F16.  K a multiple of 128.
+ */
+int g9_moe_a8w8(const void* a, const void* b, void* c, const int32_t* expert_offsets, const float* a_scale,
+                const float* b_scales, int64_t T, int64_t N, int64_t K, int64_t E, int64_t stride_am,
+                int64_t stride_bn, int64_t stride_be, int64_t stride_cm, int out_dtype, void* stream);
+
+/*
  * g9_moe_a4w4: MXFP4 as g9_gemm_a4w4 (strides in bytes); expert e's weights are
  * b + e * stride_be (N x K/2 bytes) and its scales b_scales + e * stride_bse
  * (N x K/32 bytes); `out_dtype` G9_BF16 or G9_F16.  K a multiple of 256.

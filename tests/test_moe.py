@@ -51,11 +51,24 @@ def test_moe_a4w4_argument_validation():
     assert call(asc=0) == _lib.G9_ERR_LAYOUT
 
 
+def test_moe_a8w8_argument_validation():
+    lib = _lib.load()
+    T, N, K, E = 512, 256, 512, 4
+
+    def call(out=_lib.G9_BF16, K_=K, sb=FAKE):
+        return lib.g9_moe_a8w8(FAKE, FAKE, FAKE, FAKE, None, sb, T, N, K_, E, K_, K_, N * K_, N, out, None)
+
+    assert call(out=_lib.G9_FP4) == _lib.G9_ERR_DTYPE
+    assert call(K_=192) == _lib.G9_ERR_SHAPE  # K must be a multiple of 128
+    assert call(sb=FAKE + 2) == _lib.G9_ERR_LAYOUT
+
+
 def test_moe_kernel_names():
-    names = {_lib.moe_kernel_name(dt, out) for dt, out in [(_lib.G9_F16, _lib.G9_F16), (_lib.G9_BF16, _lib.G9_BF16),
-                                                          (_lib.G9_FP4, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_F16)]}
-    assert len(names) == 4 and all(n and n.endswith("_moe_4w") for n in names)
-    assert _lib.moe_kernel_name(_lib.G9_BF8, _lib.G9_BF16) is None
+    pairs = [(_lib.G9_F16, _lib.G9_F16), (_lib.G9_BF16, _lib.G9_BF16), (_lib.G9_BF8, _lib.G9_BF16),
+             (_lib.G9_BF8, _lib.G9_F16), (_lib.G9_FP4, _lib.G9_BF16), (_lib.G9_FP4, _lib.G9_F16)]
+    names = {_lib.moe_kernel_name(dt, out) for dt, out in pairs}
+    assert len(names) == 6 and all(n and n.endswith("_moe_4w") for n in names)
+    assert _lib.moe_kernel_name(_lib.G9_F16, _lib.G9_BF16) is None
 
 
 def moe_find(off, E, T, mt):

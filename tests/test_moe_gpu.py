@@ -10,8 +10,9 @@ import torch
 
 from gfx950_gluon_tutorials_amd import quant
 from gfx950_gluon_tutorials_amd.gemm.intra_wave.a4w4 import matmul as a4w4_matmul
+from gfx950_gluon_tutorials_amd.gemm.intra_wave.a8w8 import matmul as a8w8_matmul
 from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as a16w16_matmul
-from gfx950_gluon_tutorials_amd.gemm.moe import moe_matmul, moe_matmul_a4w4
+from gfx950_gluon_tutorials_amd.gemm.moe import moe_matmul, moe_matmul_a4w4, moe_matmul_a8w8
 from oracle import gemm_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +130,29 @@ def test_moe_many_experts_multi_pass_lookup(gpu):
     for e in (5, 70, 129):
         lo, hi = int(o[e]), int(o[e + 1])
         np.testing.assert_array_equal(_bits(c[lo:hi]), _bits(a16w16_matmul(a[lo:hi].contiguous(), b[e].T)))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_moe_a8w8_matches_dense_per_expert(gpu, out_dtype):
+    _say(f"moe a8w8 {out_dtype} counts {COUNTS}")
+    g = torch.Generator().manual_seed(16)
+    E, N, K = len(COUNTS), 384, 512
+    T = sum(COUNTS)
+    qa, sa = quant.quantize_e5m2(torch.randn(T, K, generator=g))
+    qbs, sbs = zip(*[quant.quantize_e5m2(torch.randn(N, K, generator=g) * (1 + e)) for e in range(E)])
+    qb, sb = torch.stack(qbs).to(gpu), torch.stack([s.reshape(()) for s in sbs]).float().to(gpu)
+    qa, sa = qa.to(gpu), sa.to(gpu)
+    off = _offsets(COUNTS, gpu)
+    c = moe_matmul_a8w8(qa, qb, off, a_scale=sa, b_scales=sb, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    o = off.cpu().numpy()
+    for e in range(E):
+        lo, hi = int(o[e]), int(o[e + 1])
+        if hi > lo:
+            dense = a8w8_matmul(qa[lo:hi].contiguous(), qb[e].T, a_scale=sa, b_scale=sb[e], out_dtype=out_dtype)
+            np.testing.assert_array_equal(_bits(c[lo:hi]), _bits(dense), err_msg=f"expert {e}")
+    codes = lambda t: t.view(torch.uint8).cpu().numpy()
+    out = "bf16" if out_dtype == torch.bfloat16 else "f16"
+    ref = R.moe_ref(lambda x, y, s: R.a8w8_ref(x, y, float(sa.cpu()), s, out), codes(qa), codes(qb), o,
+                    expert_args=(sb.cpu().numpy(),))
+    assert R.rel_frobenius(c.float().cpu().numpy(), ref) <= 1e-3
