@@ -37,6 +37,11 @@
 // ends with C[m0 + l%16][n0 + 4*(l/16) + 0..3]: four consecutive output
 // columns, which the epilogue writes to LDS as one 8-byte store and then streams
 // out as coalesced 16-byte row chunks.
+//
+// Three tile schedules drive this pipeline: gemm_dp (one tile per workgroup),
+// gemm_sk (persistent workgroups over (tile, stage) ranges with a K-ordered
+// fp32 fixup, bit-identical to gemm_dp) and gemm_moe (tiles grouped by
+// expert, each expert with its own rows of A and C and its own B).
 #pragma once
 
 #include <type_traits>
