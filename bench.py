@@ -74,6 +74,8 @@ def parse_args():
     p.add_argument("--only", default="", help="run one case only, e.g. fp16 (for profilers)")
     p.add_argument("--telemetry-s", type=float, default=3.0,
                    help="run the headline case this long while sampling board power and clock (0: skip)")
+    p.add_argument("--ksweep", type=int, default=0,
+                   help="instead: time fp16/bf8/mxfp4 at M=N=4096 over the reference benches' K sweep, 4 and 8 waves")
     p.add_argument("--pair", type=int, default=0,
                    help="profiler target: run our 4-wave kernel and hipBLASLt on the --only dtype (fp16 by "
                         "default) N times each at 4096x4096x8192, then exit")
@@ -436,6 +438,44 @@ def make_moe_case(dtype: str, dev, nsets: int, seed: int = 8):
     return launch, counts
 
 
+# K sweep of the reference benches (kernels/gemm/intra_wave/a16w16/bench.py:85-95, a8w8/bench.py:73-82,
+# a4w4/bench.py:167-177) and the reference's published TFLOPS at M=N=4096 (4-wave, 8-wave):
+# kernels/gemm/inter_wave/a16w16/README.md:120-122, inter_wave/a8w8/README.md:61-63,
+# inter_wave/a4w4/v0_sliceMN/README.md:60-62 (4-wave) and inter_wave/a4w4/README.md:13-21 (8-wave, v2).
+KSWEEP = {
+    "fp16": [512, 1024, 2048, 3072, 4096, 8192, 16384, 32768],
+    "bf8": [1024, 2048, 3072, 4096, 8192, 16384, 32768],
+    "mxfp4": [1024, 2048, 3072, 4096, 8192, 16384, 32768, 65536],
+}
+KSWEEP_REF = {
+    "fp16": {8192: (1608, 1478), 16384: (1651, 1529), 32768: (1432, 1328)},
+    "bf8": {8192: (3215, 2949), 16384: (3476, 3131), 32768: (3090, 3202)},
+    "mxfp4": {8192: (4986, 4479), 16384: (5550, 4900), 32768: (5804, 5196)},
+}
+
+
+def ksweep(args, dev) -> dict:
+    import torch
+
+    seeds = {"fp16": 1, "bf8": 2, "mxfp4": 3}
+    out = {}
+    for dt, ks in KSWEEP.items():
+        for kk in ks:
+            for w in (4, 8):
+                rotate = args.rotate_mb if kk < 16384 else max(args.rotate_mb, 2048)
+                nsets = max(2, -(-rotate * 2**20 // set_bytes(dt, 4096, 4096, kk)))
+                launch = make_case(dt, 4096, 4096, kk, seeds[dt], dev, nsets, w)
+                ms = time_case(launch, max(20, args.steps // 2), args.warmup // 2, settle_s=args.settle_ms / 2e3)
+                tf = 2.0 * 4096 * 4096 * kk / (ms * 1e-3) / 1e12
+                ref = KSWEEP_REF[dt].get(kk, (None, None))[0 if w == 4 else 1]
+                out[f"{dt}_k{kk}_{w}w"] = {"tflops": round(tf, 2), "ms": round(ms, 5), "reference_tflops": ref}
+                print(f"# ksweep {dt:5s} K={kk:<6d} {w}w: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOPS"
+                      + (f"  | reference {ref}" if ref else ""), flush=True)
+                del launch
+                torch.cuda.empty_cache()
+    return out
+
+
 def make_vendor_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
     """launch(i) running ROCm's library GEMM (hipBLASLt through torch) on the
     same kind of operands as make_case: torch.matmul for fp16/bf16,
@@ -500,6 +540,9 @@ def main():
     dev = torch.device("cuda:0")
     M = N = 4096
     K = 8192
+    if args.ksweep:
+        print(json.dumps({"ksweep": ksweep(args, dev)}))
+        return
     if args.pair:
         dt = args.only or "fp16"
         seed = {"fp16": 1, "bf16": 1, "bf8": 2}[dt]
