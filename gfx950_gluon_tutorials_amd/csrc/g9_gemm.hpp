@@ -407,8 +407,11 @@ G9_DEV void static_for(F&& f) {
 // a window of W slots, so the region-closing lgkmcnt(0) finds them complete;
 // the DMAs are spread over the whole region.  FP4 reads one scale word per
 // fragment after the first reads; with 16x16 fragments it then gathers the
-// bytes each MFMA step needs at slot kPermQ, after its reads and well before
-// the next region's MFMAs read the results.
+// bytes each MFMA step needs, one fragment per slot in the slots perm_q(F)
+// just before the region's last (a block-scaled MFMA leaves one issue slot
+// beside it, so four permutes in one slot held up the MFMA stream: spreading
+// them measured ~1% faster), after the reads and before the next region's
+// MFMAs read the results.
 template <Op OP, class G, int NF>
 struct Slots {
   static constexpr int NM = Shape<OP, G>::NM;
@@ -423,10 +426,10 @@ struct Slots {
   static constexpr int dma_q(int J) { return NQ == 1 ? 0 : 1 + J * (NQ - 1) / D; }
   static constexpr int kScaleDmaQ = dma_q(D - 1) + 2 < NQ ? dma_q(D - 1) + 2 : NQ - 1;
   static constexpr int kLastQ = (read_q(NR - 1) > scale_q(NF - 1) ? read_q(NR - 1) : scale_q(NF - 1)) + 3;
-  static constexpr int kPermQ = (kLastQ > NQ - 8 ? kLastQ : NQ - 8) < NQ - 1 ? (kLastQ > NQ - 8 ? kLastQ : NQ - 8)
-                                                                              : NQ - 1;
+  static constexpr int perm_q(int F) { return NQ - NF - 1 + F; }
   static_assert(NQ >= 1, "a region needs an MFMA after its barrier");
   static_assert(!OpInfo<OP>::kScaled || scale_q(NF - 1) < NQ, "scale reads must fit the region");
+  static_assert(!OpInfo<OP>::kScaled || G::MD != 16 || perm_q(0) >= kLastQ, "permutes must follow the scale reads");
 };
 
 // Keeps a value in a register the compiler cannot see through, so constant
@@ -631,11 +634,16 @@ struct Pipe {
           std::make_integer_sequence<int, NF>{});
     }
   }
+  // Packs fragment F's two scale bytes of each MFMA step into one register
+  // (byte e = step e), so the MFMA selects its scale with op_sel.
+  template <int X, int F>
+  G9_DEV void gather_one(FragSet<G>& f) const {
+    f[F].sp = __builtin_amdgcn_perm(f[F].sc.y, f[F].sc.x, sel);
+  }
   template <int X>
   G9_DEV void gather_scales(FragSet<G>& f) const {
     constexpr int NF = X < 2 ? G::FM : G::FN;
-#pragma unroll
-    for (int i = 0; i < NF; ++i) f[i].sp = __builtin_amdgcn_perm(f[i].sc.y, f[i].sc.x, sel);
+    static_for<NF>([&](auto F) { gather_one<X, decltype(F)::value>(f); });
   }
 };
 
@@ -713,9 +721,14 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
       if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
     });
     if constexpr (part >= 0 && q == S::kScaleDmaQ) P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, ms);
-    if constexpr (OpInfo<OP>::kScaled && G::MD == 16 && q == S::kPermQ) {
-      waitcnt<63, 0>();
-      P.template gather_scales<RX>(nxt);
+    if constexpr (OpInfo<OP>::kScaled && G::MD == 16) {
+      static_for<NF>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        if constexpr (S::perm_q(f) == q) {
+          if constexpr (f == 0) waitcnt<63, 0>();  // the region's scale reads landed
+          P.template gather_one<RX, f>(nxt);
+        }
+      });
     }
   }
   __builtin_amdgcn_sched_barrier(0);
