@@ -35,8 +35,10 @@ G9_FP4 = 3
 # Schedules.
 G9_SCHED_DP = 0
 G9_SCHED_SK = 1
+G9_SCHED_SPLITK = 2
 
-SCHEDULES = {"dp": G9_SCHED_DP, "data_parallel": G9_SCHED_DP, "sk": G9_SCHED_SK, "streamk": G9_SCHED_SK}
+SCHEDULES = {"dp": G9_SCHED_DP, "data_parallel": G9_SCHED_DP, "sk": G9_SCHED_SK, "streamk": G9_SCHED_SK,
+             "splitk": G9_SCHED_SPLITK, "split_k": G9_SCHED_SPLITK}
 
 # Exported symbols and their signatures; the CPU test checks the library
 # exports exactly these.
@@ -63,6 +65,7 @@ SIGNATURES = {
     "g9_kernel_name": (ctypes.c_char_p, [_int, _int, _int, _int]),
     "g9_status_string": (ctypes.c_char_p, [_int]),
     "g9_streamk_workgroups": (_int, []),
+    "g9_splitk_factor": (_int, [ctypes.c_int64, _int, _int]),
     "g9_version": (_int, []),
 }
 

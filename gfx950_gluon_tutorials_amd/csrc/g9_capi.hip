@@ -49,6 +49,24 @@ G9_DEFINE_MOE(g9_a8w8_f16out, Op::BF8, OUT_F16)
 G9_DEFINE_MOE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
 G9_DEFINE_MOE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
+// Split-K kernels: the segment kernel depends only on the operand type (its
+// output is fp32 partials), the reduction only on the output type.
+#define G9_DEFINE_SPLITK(NAME, OP)                                                                 \
+  extern "C" __global__ G9_ATTRS(Geo4<kMfmaDim<OP>>) void NAME##_splitk_4w(GemmParams p) {       \
+    gemm_splitk<OP, Geo4<kMfmaDim<OP>>>(p);                                                        \
+  }                                                                                                \
+  extern "C" __global__ G9_ATTRS(Geo8<kMfmaDim8<OP>>) void NAME##_splitk_8w(GemmParams p) {      \
+    gemm_splitk<OP, Geo8<kMfmaDim8<OP>>>(p);                                                       \
+  }
+
+G9_DEFINE_SPLITK(g9_a16w16_f16, Op::F16)
+G9_DEFINE_SPLITK(g9_a16w16_bf16, Op::BF16)
+G9_DEFINE_SPLITK(g9_a8w8, Op::BF8)
+G9_DEFINE_SPLITK(g9_a4w4, Op::FP4)
+
+extern "C" __global__ __launch_bounds__(256) void g9_splitk_reduce_f16(GemmParams p) { splitk_reduce<OUT_F16>(p); }
+extern "C" __global__ __launch_bounds__(256) void g9_splitk_reduce_bf16(GemmParams p) { splitk_reduce<OUT_BF16>(p); }
+
 typedef void (*KernelFn)(GemmParams);
 
 namespace {
@@ -72,6 +90,17 @@ const KernelEntry kKernels[] = {
     G9_ENTRY(G9_FP4, G9_BF16, g9_a4w4_bf16out),  G9_ENTRY(G9_FP4, G9_F16, g9_a4w4_f16out),
 };
 
+#define G9_SPLITK_ENTRY(DT, OUT, NAME)                                                              \
+  {DT, OUT, G9_SCHED_SPLITK, 4, NAME##_splitk_4w, #NAME "_splitk_4w"}, {                           \
+    DT, OUT, G9_SCHED_SPLITK, 8, NAME##_splitk_8w, #NAME "_splitk_8w"                              \
+  }
+
+const KernelEntry kSplitKernels[] = {
+    G9_SPLITK_ENTRY(G9_F16, G9_F16, g9_a16w16_f16),  G9_SPLITK_ENTRY(G9_BF16, G9_BF16, g9_a16w16_bf16),
+    G9_SPLITK_ENTRY(G9_BF8, G9_F16, g9_a8w8),        G9_SPLITK_ENTRY(G9_BF8, G9_BF16, g9_a8w8),
+    G9_SPLITK_ENTRY(G9_FP4, G9_BF16, g9_a4w4),       G9_SPLITK_ENTRY(G9_FP4, G9_F16, g9_a4w4),
+};
+
 const KernelEntry kMoeKernels[] = {
     {G9_F16, G9_F16, G9_SCHED_DP, 4, g9_a16w16_f16_moe_4w, "g9_a16w16_f16_moe_4w"},
     {G9_BF16, G9_BF16, G9_SCHED_DP, 4, g9_a16w16_bf16_moe_4w, "g9_a16w16_bf16_moe_4w"},
@@ -89,6 +118,8 @@ const KernelEntry* find_moe_kernel(int dtype, int out) {
 
 const KernelEntry* find_kernel(int dtype, int out, int sched, int waves) {
   for (const KernelEntry& k : kKernels)
+    if (k.dtype == dtype && k.out == out && k.sched == sched && k.waves == waves) return &k;
+  for (const KernelEntry& k : kSplitKernels)
     if (k.dtype == dtype && k.out == out && k.sched == sched && k.waves == waves) return &k;
   return nullptr;
 }
@@ -132,12 +163,23 @@ int cu_count() {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Split-K workspace layout: the header, then a flag region as large as the
+// one g9_workspace_init clears for a workspace of this size (the flags of any
+// stream-K launch that fits it), then the partials.  Split-K never writes the
+// header or the flags, so one workspace serves both schedules.
+size_t splitk_base(size_t ws_bytes) {
+  return kWsHeader + flags_bytes((long long)((ws_bytes - kWsHeader) / kWsTileBytes + 1));
+}
+size_t splitk_bytes(long long partials) {
+  return kWsHeader + flags_bytes(partials + 1) + (size_t)partials * kWsTileBytes;
+}
+
 // Shared launch path.  Sizes/strides were validated by the caller except the
 // generic checks done here.
 int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
            void* stream) {
   if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
-  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK) return G9_ERR_SCHEDULE;
+  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK) return G9_ERR_SCHEDULE;
   const KernelEntry* k = find_kernel(dtype, out, schedule, waves);
   if (!k) return G9_ERR_DTYPE;
   p.tiles_m = (p.M + kTile - 1) / kTile;
@@ -147,7 +189,32 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
   const long long tiles = (long long)p.tiles_m * p.tiles_n;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int grid;
-  if (schedule == G9_SCHED_DP) {
+  if (schedule == G9_SCHED_SPLITK) {
+    const int cus = cu_count();
+    if (cus <= 0) return G9_ERR_HIP;
+    const int S = g9_splitk_factor(tiles, p.ns, cus);
+    if (S <= 1) {
+      // The grid fills the chip (or K is one stage): run the data-parallel kernel.
+      k = find_kernel(dtype, out, G9_SCHED_DP, waves);
+      grid = (int)tiles;
+    } else {
+      if (!ws || ws_bytes < splitk_bytes(tiles * S) || !aligned(ws, 256)) return G9_ERR_WORKSPACE;
+      const size_t base = splitk_base(ws_bytes);
+      if (base + (size_t)(tiles * S) * kWsTileBytes > ws_bytes) return G9_ERR_WORKSPACE;
+      p.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + base);
+      p.split = S;
+      void* args[] = {&p};
+      if (hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3((int)(tiles * S)), dim3(64 * waves), args, 0,
+                          s) != hipSuccess)
+        return G9_ERR_HIP;
+      const long long threads = (long long)p.M * p.tiles_n * (kTile / 8);
+      const KernelFn red = out == G9_BF16 ? g9_splitk_reduce_bf16 : g9_splitk_reduce_f16;
+      return hipLaunchKernel(reinterpret_cast<const void*>(red), dim3((int)((threads + 255) / 256)), dim3(256), args,
+                             0, s) == hipSuccess
+                 ? G9_OK
+                 : G9_ERR_HIP;
+    }
+  } else if (schedule == G9_SCHED_DP) {
     grid = (int)tiles;
   } else {
     const size_t need = kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
@@ -404,11 +471,36 @@ const char* g9_moe_kernel_name(int dtype, int out_dtype) {
 }
 
 size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves) {
-  (void)K;
   (void)waves;
-  if (schedule != G9_SCHED_SK || M <= 0 || N <= 0 || stage_k(dtype) == 0) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || stage_k(dtype) == 0) return 0;
   const long long tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
+  if (schedule == G9_SCHED_SPLITK) {
+    const int cus = cu_count();
+    const int S = cus > 0 ? g9_splitk_factor(tiles, (int)(K / stage_k(dtype)), cus) : 1;
+    return S > 1 ? splitk_bytes(tiles * S) : 0;
+  }
+  if (schedule != G9_SCHED_SK) return 0;
   return kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
+}
+
+// Split factor from a cost model in units of one K stage (~2048 MFMA cycles):
+// data-parallel costs its one tile chain plus the epilogue (~4); split-K with
+// S segments costs one segment (one wave of tiles * S <= cus workgroups) plus
+// ~7 for its prologue and partial store, plus ~0.04 per 256 KiB partial the
+// reduction reads at full-chip bandwidth.  Grids that fill half the chip, and
+// factors past 16, are not split.
+int g9_splitk_factor(int64_t tiles, int stages, int cus) {
+  if (tiles <= 0 || stages < 2 || cus <= 0 || tiles * 2 > cus) return 1;
+  int best = 1;
+  long long best_cost = 100LL * stages + 400;
+  for (int S = 2; S <= 16 && S <= stages && tiles * S <= cus; ++S) {
+    const long long cost = 100LL * ((stages + S - 1) / S) + 700 + 4LL * S * tiles;
+    if (cost < best_cost) {
+      best = S;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 }  // extern "C"
@@ -469,7 +561,7 @@ const char* g9_status_string(int status) {
     case G9_ERR_SCHEDULE:
       return "unsupported schedule or wave count";
     case G9_ERR_WORKSPACE:
-      return "stream-K workspace missing or too small";
+      return "stream-K / split-K workspace missing or too small";
     case G9_ERR_HIP:
       return "HIP launch failed";
   }

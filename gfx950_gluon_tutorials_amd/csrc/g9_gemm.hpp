@@ -137,6 +137,8 @@ struct GemmParams {
   u32 epoch;
   int* err;                   // set to 1 when a flag wait times out
   int sk_ctas;                // persistent workgroups
+  // split-K: K segments per tile (the partials go to ws)
+  int split;
   // grouped (MoE) GEMM: expert e owns rows [moe_off[e], moe_off[e+1]) of A
   // and C and its own B (and FP4 B scales) moe_b_stride (moe_bsc_stride)
   // bytes after expert e - 1's
@@ -1143,6 +1145,96 @@ G9_DEV void gemm_sk(const GemmParams& p) {
   }
   sk_stamp(2);
   sk_times_store(times);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K schedule, for grids with too few tiles to fill the chip.
+//
+// Each tile's K stages are cut into `split` contiguous segments of near-equal
+// length, one workgroup per (segment, tile).  Segment s writes its fp32
+// partial tile into the s-th of `split` row-major fp32 matrices of
+// tiles_m*256 x tiles_n*256 in the workspace; a second kernel sums the
+// segments' partials in segment order, applies the epilogue scale and rounds
+// to the output type.  The order of the sum is fixed, so the result is
+// deterministic, but it is not bit-identical to the data-parallel kernel,
+// whose accumulation runs over K in one chain.
+// ---------------------------------------------------------------------------
+template <class G>
+G9_DEV void store_partial(const GemmParams& p, float* part, int tm, int tn, Acc<G>& acc) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  const int rr = lane % G::MD, gi = lane / G::MD;
+  const size_t np = (size_t)p.tiles_n * kTile;
+#pragma unroll
+  for (int qm = 0; qm < 2; ++qm)
+#pragma unroll
+    for (int qn = 0; qn < 2; ++qn)
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::FN; ++j)
+          static_for<G::NB>([&](auto B) {
+            constexpr int b = decltype(B)::value;
+            // The quad holds 4 consecutive columns of one row (the layout
+            // store_tile also uses), so each store is 16 contiguous bytes.
+            const size_t m = (size_t)tm * kTile + qm * 128 + wm * G::FM * G::MD + i * G::MD + rr;
+            const size_t n = (size_t)tn * kTile + qn * 128 + wn * G::FN * G::MD + j * G::MD + 4 * G::NG * b + 4 * gi;
+            *reinterpret_cast<f32x4*>(part + m * np + n) = get_quad<b>(acc[qm][qn][i][j]);
+          });
+}
+
+template <Op OP, class G>
+G9_DEV void gemm_splitk(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes<OpInfo<OP>::kScaled>];
+  const int S = p.split;
+  // The segments are laid out as S stacked copies of the tile grid, so the
+  // XCD remap and GROUP_SIZE_M swizzle keep tiles of one segment (one K range)
+  // together on an XCD.
+  int vm, tn;
+  tile_coords(blockIdx.x, p.tiles_m * S * p.tiles_n, p.tiles_m * S, p.tiles_n, p.num_xcds, p.group_m, vm, tn);
+  const int seg = vm / p.tiles_m, tm = vm - seg * p.tiles_m;
+  const int sb = (int)((long long)seg * p.ns / S), se = (int)((long long)(seg + 1) * p.ns / S);
+  Acc<G> acc;
+  zero_acc<G>(acc);
+  pin_acc<G>(acc);
+  mainloop<OP, G>(p, smem, tm, tn, sb, se, acc);
+  float* part = p.ws + (size_t)seg * ((size_t)p.tiles_m * kTile) * ((size_t)p.tiles_n * kTile);
+  store_partial<G>(p, part, tm, tn, acc);
+}
+
+// One thread per 8 output columns of one row: the segments' partials summed
+// in segment order, times the epilogue scale (BF8's per-tensor scales; 1
+// otherwise), rounded to 16 bits; rows >= M and columns >= N are not written.
+template <int OUT>
+G9_DEV void splitk_reduce(const GemmParams& p) {
+  const long long np = (long long)p.tiles_n * kTile;
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long m = t / (np / 8);
+  const int n = (int)(t - m * (np / 8)) * 8;
+  if (m >= p.M || n >= p.N) return;
+  const size_t seg = (size_t)p.tiles_m * kTile * (size_t)np;
+  const float* src = p.ws + (size_t)m * np + n;
+  f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.split; ++s) {
+    lo += *reinterpret_cast<const f32x4*>(src + s * seg);
+    hi += *reinterpret_cast<const f32x4*>(src + s * seg + 4);
+  }
+  float scale = 1.f;
+  if (p.a_scale) scale *= *p.a_scale;
+  if (p.b_scale) scale *= *p.b_scale;
+  lo *= scale;
+  hi *= scale;
+  const u32x2 l = OUT == OUT_BF16 ? pack4_bf16(lo) : pack4_f16(lo);
+  const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(hi) : pack4_f16(hi);
+  const u32x4 d = {l.x, l.y, h.x, h.y};
+  char* dst = p.c + ((size_t)m * p.ldc + n) * 2;
+  if (n + 8 <= p.N && ((uintptr_t)dst & 15) == 0) {
+    *reinterpret_cast<u32x4*>(dst) = d;
+  } else {
+    const uint16_t* hv = reinterpret_cast<const uint16_t*>(&d);
+    for (int e = 0; e < 8; ++e)
+      if (n + e < p.N) reinterpret_cast<uint16_t*>(dst)[e] = hv[e];
+  }
 }
 
 }  // namespace g9

@@ -58,7 +58,7 @@ def _schedule_code(schedule, M: int, N: int, dtype: int) -> int:
     try:
         return _lib.SCHEDULES[name]
     except KeyError:
-        raise ValueError(f"unknown schedule {schedule!r} (expected 'dp', 'streamk' or 'auto')") from None
+        raise ValueError(f"unknown schedule {schedule!r} (expected 'dp', 'streamk', 'splitk' or 'auto')") from None
 
 
 def _require_device(*tensors: torch.Tensor) -> torch.device:

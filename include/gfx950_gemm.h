@@ -5,14 +5,17 @@
  * ("NT": A is M rows of K values, B is N rows of K values).  Three operand
  * types: FP16/BF16 (a16w16), BF8 = fp8 e5m2 with optional per-tensor fp32
  * scales (a8w8), and MXFP4 = e2m1 packed two per byte with one E8M0 scale per
- * 32 K-values (a4w4).  Two tile schedules: data-parallel (one 256x256 tile per
- * workgroup) and stream-K (persistent workgroups over (tile, K-stage) work with
- * a K-ordered fp32 fixup; bit-identical to data-parallel).
+ * 32 K-values (a4w4).  Three tile schedules: data-parallel (one 256x256 tile per
+ * workgroup), stream-K (persistent workgroups over (tile, K-stage) work with
+ * a K-ordered fp32 fixup; bit-identical to data-parallel) and split-K (for
+ * grids of fewer tiles than half the CUs: each tile's K range is cut into
+ * segments computed in parallel and their fp32 partials are summed in a fixed
+ * order by a second kernel; deterministic, within rounding of data-parallel).
  *
  * Every entry point takes raw device pointers, sizes and strides in ELEMENTS
  * (bytes for the uint8 MXFP4 operands and scales), launches asynchronously on
  * `stream` (a hipStream_t; NULL = default stream) and returns a status code.
- * Nothing is synchronised and nothing is allocated: the stream-K workspace is
+ * Nothing is synchronised and nothing is allocated: the stream-K / split-K workspace is
  * owned by the caller (size from g9_workspace_size, zeroed once with
  * g9_workspace_init before first use, and not shared by launches that may run
  * concurrently).
@@ -38,15 +41,17 @@ enum {
   G9_ERR_LAYOUT = 2,    /* K stride != 1, N stride of C != 1, operand rows not 16-byte aligned */
   G9_ERR_DTYPE = 3,     /* unsupported element / output type */
   G9_ERR_SCHEDULE = 4,  /* unknown schedule or wave count */
-  G9_ERR_WORKSPACE = 5, /* stream-K workspace missing or too small */
+  G9_ERR_WORKSPACE = 5, /* stream-K / split-K workspace missing or too small */
   G9_ERR_HIP = 6        /* the HIP runtime rejected the launch */
 };
 
 /* Element / output types. */
 enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3 };
 
-/* Tile schedules. */
-enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1 };
+/* Tile schedules.  G9_SCHED_SPLITK has no counterpart in the reference: it is
+ * for callers whose grids leave most CUs idle (few-row GEMMs, one GPU's
+ * shard of a sharded GEMM). */
+enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1, G9_SCHED_SPLITK = 2 };
 
 /*
  * a16w16: FP16 or BF16 (`dtype` = G9_F16 / G9_BF16) in and out, fp32 accumulate.
@@ -133,9 +138,11 @@ int g9_moe_a4w4(const void* a, const void* b, void* c, const void* a_scales, con
 const char* g9_moe_kernel_name(int dtype, int out_dtype);
 
 /*
- * Bytes of stream-K workspace a call with these arguments needs (0 for the
- * data-parallel schedule).  `dtype` is the operand type.
- * No counterpart in the reference (it has no stream-K schedule).
+ * Bytes of workspace a call with these arguments needs (0 for the
+ * data-parallel schedule, and for split-K when it runs as data-parallel).
+ * `dtype` is the operand type.  Split-K's size depends on the current
+ * device's CU count.  No counterpart in the reference (it has neither
+ * stream-K nor split-K).
  */
 size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves);
 
@@ -164,6 +171,13 @@ const char* g9_status_string(int status);
 
 /* Number of persistent workgroups the stream-K schedule launches on the current device. */
 int g9_streamk_workgroups(void);
+
+/*
+ * K segments per tile the split-K schedule uses for `tiles` output tiles of
+ * `stages` K stages on a device of `cus` CUs (1 = it runs as data-parallel).
+ * Pure function of its arguments.  No counterpart in the reference.
+ */
+int g9_splitk_factor(int64_t tiles, int stages, int cus);
 
 /* Library ABI version (major * 100 + minor). */
 int g9_version(void);

@@ -68,6 +68,46 @@ def test_kernel_names_are_stable_and_unique():
     assert _lib.kernel_name(_lib.G9_F16, _lib.G9_BF16, 0, 4) is None
 
 
+def test_splitk_kernel_names():
+    # One segment kernel per operand type and wave count (its output is fp32
+    # partials, so both output types of BF8 / MXFP4 share it).
+    for dt, out, stem in [(_lib.G9_F16, _lib.G9_F16, "g9_a16w16_f16"), (_lib.G9_BF16, _lib.G9_BF16, "g9_a16w16_bf16"),
+                          (_lib.G9_BF8, _lib.G9_F16, "g9_a8w8"), (_lib.G9_BF8, _lib.G9_BF16, "g9_a8w8"),
+                          (_lib.G9_FP4, _lib.G9_BF16, "g9_a4w4"), (_lib.G9_FP4, _lib.G9_F16, "g9_a4w4")]:
+        for waves in (4, 8):
+            assert _lib.kernel_name(dt, out, _lib.G9_SCHED_SPLITK, waves) == f"{stem}_splitk_{waves}w"
+
+
+@pytest.mark.parametrize("tiles,stages,cus,want", [
+    (32, 128, 256, 8),    # one GPU's shard of a 4096-row GEMM over 8 GPUs: 512 x 4096, K = 8192 fp16
+    (2, 64, 256, 16),     # a few-row GEMM: capped at 16 segments
+    (128, 128, 256, 2),   # half the CUs: two segments per tile still fill the chip
+    (129, 128, 256, 1),   # more than half the CUs busy already: data-parallel
+    (160, 128, 256, 1),
+    (4, 1, 256, 1),       # one K stage cannot be split
+    (4, 3, 256, 1),       # too few stages to pay for a segment's prologue and partial store
+    (4, 40, 256, 14),     # 14 segments of <= 3 stages cost less than 16 (still 3 stages, more partials)
+    (0, 64, 256, 1),
+])
+def test_splitk_factor_known_answers(tiles, stages, cus, want):
+    assert _lib.load().g9_splitk_factor(tiles, stages, cus) == want
+
+
+def test_splitk_factor_invariants():
+    lib = _lib.load()
+    for cus in (80, 256, 304):
+        for tiles in (1, 2, 3, 7, 16, 31, 64, 100, 151, 200, 1000):
+            for stages in (1, 2, 5, 16, 32, 128, 512):
+                s = lib.g9_splitk_factor(tiles, stages, cus)
+                assert 1 <= s <= 16 and s <= max(stages, 1)
+                assert s == 1 or tiles * s <= cus
+                if 2 * tiles > cus:
+                    assert s == 1
+                # The model never picks a split that costs more than data-parallel.
+                if s > 1:
+                    assert 100 * (-(-stages // s)) + 700 + 4 * s * tiles < 100 * stages + 400
+
+
 def test_workspace_size():
     lib = _lib.load()
     assert lib.g9_workspace_size(_lib.G9_F16, 4096, 4096, 8192, _lib.G9_SCHED_DP, 4) == 0
