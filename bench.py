@@ -16,7 +16,8 @@ TFLOPS = 2*M*N*K / t.
 The JSON line also carries the roofline of the dominant kernel (MFMA-bound:
 achieved TFLOP/s vs the published dense peak) with the HBM traffic per launch
 read from the committed rocprof counter summary when present, the other
-dtypes and the stream-K shapes, and a CPU baseline: the oracle's fp32 GEMM
+dtypes, the stream-K shapes, split-K against data-parallel on grids of 16-128
+tiles, the grouped (MoE) GEMMs, and a CPU baseline: the oracle's fp32 GEMM
 of the dequantized operands timed on this host on a bounded row sample.
 """
 
@@ -61,6 +62,8 @@ def parse_args():
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
     p.add_argument("--waves", default="4,8", help="wave schedules to time: 4 (1 wave/SIMD), 8 (2 waves/SIMD)")
     p.add_argument("--moe", type=int, default=1, help="also time the grouped (MoE) GEMMs (0/1)")
+    p.add_argument("--splitk", type=int, default=1,
+                   help="also time split-K against data-parallel on grids of <= 128 tiles (0/1)")
     p.add_argument("--vendor", type=int, default=1,
                    help="also time ROCm's hipBLASLt (torch.matmul / torch._scaled_mm) on the same shapes, "
                         "interleaved with ours, for fp16/bf16/bf8 at K=8192 (0/1)")
@@ -635,6 +638,32 @@ def main():
                   flush=True)
             del launch
             torch.cuda.empty_cache()
+    splitk = {}
+    if args.splitk and not args.only:
+        from gfx950_gluon_tutorials_amd import _lib
+
+        lib = _lib.load()
+        codes = {"fp16": _lib.G9_F16, "bf8": _lib.G9_BF8, "mxfp4": _lib.G9_FP4}
+        stage_k = {"fp16": 64, "bf8": 128, "mxfp4": 256}
+        # Few-row GEMMs and one GPU's shard of a row-sharded 4096 x 4096 x 8192
+        # GEMM (512 rows = 1/8): 16-128 tiles, so data-parallel leaves CUs idle.
+        for (dt, m, n, k) in [("fp16", 256, 4096, 8192), ("fp16", 512, 4096, 8192), ("fp16", 1024, 4096, 8192),
+                              ("fp16", 2048, 4096, 8192), ("bf8", 512, 4096, 8192), ("mxfp4", 512, 4096, 8192)]:
+            launch = make_case(dt, m, n, k, 5, dev, max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, m, n, k))))
+            ms_dp = time_case(launch, max(20, args.steps // 2), 20, "dp", 0.3)
+            ms_sp = time_case(launch, max(20, args.steps // 2), 20, "splitk", 0.3)
+            flop = 2.0 * m * n * k
+            tiles = -(-m // 256) * -(-n // 256)
+            S = lib.g9_splitk_factor(tiles, k // stage_k[dt], lib.g9_streamk_workgroups())
+            ws = lib.g9_workspace_size(codes[dt], m, n, k, _lib.G9_SCHED_SPLITK, 4)
+            splitk[f"{dt}_{m}x{n}x{k}"] = {"dp_tflops": round(flop / ms_dp / 1e9, 2),
+                                           "splitk_tflops": round(flop / ms_sp / 1e9, 2), "dp_ms": round(ms_dp, 5),
+                                           "splitk_ms": round(ms_sp, 5), "tiles": tiles, "split": S,
+                                           "workspace_bytes": ws}
+            print(f"# split-K {dt} {m}x{n}x{k} ({tiles} tiles, {S} segments): dp {flop / ms_dp / 1e9:.1f}  "
+                  f"splitk {flop / ms_sp / 1e9:.1f} TFLOPS ({ms_dp / ms_sp:.2f}x)", flush=True)
+            del launch
+            torch.cuda.empty_cache()
     moe = {}
     if args.moe and not args.only:
         E, T, N, K_ = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
@@ -679,6 +708,7 @@ def main():
                      "frac": r["frac_of_peak"], "traffic": load_traffic(f"{head}_{M}x{N}x{K}")},
         "per_dtype": results,
         "streamk": sk,
+        "splitk": splitk,
         "moe": moe,
     }
     if args.cpu_baseline and not args.only:
