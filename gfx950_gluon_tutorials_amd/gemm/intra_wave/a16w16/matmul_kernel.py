@@ -7,7 +7,10 @@ bench passes it (kernels/gemm/intra_wave/a16w16/bench.py:208); the output has
 ``a.dtype``.  The launch is asynchronous on the current stream.
 
 ``schedule`` (keyword-only, an addition) selects the data-parallel grid
-("dp", the reference's only schedule), persistent stream-K ("streamk"), or
+("dp", the reference's only schedule), persistent stream-K ("streamk"),
+split-K ("splitk": for outputs of at most half a wave of 256x256 tiles, K cut
+into segments whose fp32 partials a second kernel sums in a fixed order;
+deterministic, within rounding of "dp", which it runs on fuller grids), or
 "auto": stream-K for outputs of more than one and at most 1.25 waves of
 256x256 tiles per CU, where it measured faster, data-parallel otherwise.
 """
