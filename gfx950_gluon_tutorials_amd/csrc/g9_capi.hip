@@ -1,6 +1,7 @@
 // extern "C" entry points of the gfx950 GEMM library (declared in
 // include/gfx950_gemm.h).  Each validates shapes, strides and alignment,
-// fills a GemmParams and launches one named kernel on the caller's stream.
+// fills a GemmParams and launches one named kernel on the caller's stream
+// (split-K: the segment kernel, then its reduction, on that stream).
 #include <atomic>
 
 #include "../../include/gfx950_gemm.h"
