@@ -332,11 +332,12 @@ def summarize_rocpd(path: str) -> None:
             rows = con.execute("select name, grid_x, duration from kernels order by start").fetchall()
             # One group per consecutive run of a kernel among the GEMM kernels
             # (the same kernel at two shapes, e.g. K=8192 and the headline K,
-            # gives two groups, the later one suffixed #2).
+            # gives two groups, the later one suffixed #2).  The split-K
+            # reduction, launched after every split-K launch, does not end a run.
             groups, runs, last = {}, {}, None
             for name, grid, dur in rows:
                 key = (name, grid)
-                if name.startswith("g9_") and key != last:
+                if name.startswith("g9_") and "splitk_reduce" not in name and key != last:
                     runs[key] = runs.get(key, 0) + 1
                     last = key
                 n = runs.get(key, 1)
@@ -359,7 +360,7 @@ def summarize_rocpd(path: str) -> None:
             groups, runs, last = {}, {}, None
             for name, grid, cn, val, dur, _ in rows:
                 key = (name, grid)
-                if name.startswith("g9_") and key != last:
+                if name.startswith("g9_") and "splitk_reduce" not in name and key != last:
                     runs[key] = runs.get(key, 0) + 1
                     last = key
                 n = runs.get(key, 1)
