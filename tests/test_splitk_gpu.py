@@ -164,3 +164,54 @@ def test_splitk_workspace_size_and_sharing_with_streamk(gpu):
         torch.cuda.synchronize()
         assert _launch.WORKSPACES.error(gpu) == 0
         assert torch.equal(sk, dp)
+
+
+def _random_shapes(n=12, seed=7):
+    """Seeded shapes of 1-128 tiles with ragged M/N and K of 2-80 stages."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M, N = int(rng.integers(1, 3000)), int(rng.integers(8, 3000))
+        if -(-M // 256) * -(-N // 256) > 128:
+            continue
+        out.append((M, N, int(rng.integers(2, 81)), int(rng.choice([4, 8])), str(rng.choice(["fp16", "bf16", "bf8", "mxfp4"]))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,stages,waves,kind", _random_shapes())
+def test_splitk_random_shapes_match_dp(gpu, M, N, stages, waves, kind):
+    """Split-K against data-parallel (the FP16 tolerance; BF8 / MXFP4: relative
+    Frobenius 1e-3 of DP's own output) on seeded ragged shapes."""
+    N = (N + 7) // 8 * 8 if kind == "mxfp4" else N
+    code = {"fp16": _lib.G9_F16, "bf16": _lib.G9_BF16, "bf8": _lib.G9_BF8, "mxfp4": _lib.G9_FP4}[kind]
+    K = stages * _launch.STAGE_K[code]
+    _say(f"split-K random {kind} {M}x{N}x{K} waves={waves} split={_factor(M, N, K, code)}")
+    g = torch.Generator().manual_seed(M * 7919 + N)
+    outs = {}
+    if kind in ("fp16", "bf16"):
+        dt = torch.float16 if kind == "fp16" else torch.bfloat16
+        a = (torch.randn(M, K, generator=g) * 0.1).to(dt).to(gpu)
+        b = (torch.randn(N, K, generator=g) * 0.1).to(dt).to(gpu)
+        for sched in ("dp", "splitk"):
+            outs[sched] = _launch.gemm_a16w16(a, b.T, torch.empty(M, N, dtype=dt, device=gpu), schedule=sched,
+                                              waves=waves)
+    elif kind == "bf8":
+        qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=g))
+        qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=g))
+        for sched in ("dp", "splitk"):
+            outs[sched] = _launch.gemm_a8w8(qa.to(gpu), qb.to(gpu).T, torch.empty(M, N, dtype=torch.bfloat16, device=gpu),
+                                            a_scale=sa.to(gpu), b_scale=sb.to(gpu), schedule=sched, waves=waves)
+    else:
+        pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=g))
+        pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=g))
+        args = [t.to(gpu) for t in (pa, pb, sa, sb)]
+        for sched in ("dp", "splitk"):
+            outs[sched] = _launch.gemm_a4w4(*args, torch.empty(M, N, dtype=torch.bfloat16, device=gpu),
+                                            schedule=sched, waves=waves)
+    torch.cuda.synchronize()
+    dp = outs["dp"].float().cpu().numpy()
+    if kind in ("fp16", "bf16"):
+        _check_f16(outs["splitk"], dp, K, 0.01)
+    else:
+        err = R.rel_frobenius(outs["splitk"].float().cpu().numpy(), dp)
+        assert err <= 1e-3, f"relative Frobenius error {err:.3g} against data-parallel"
