@@ -161,7 +161,9 @@ int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stre
 
 /*
  * Name of the kernel a call with this (dtype, out_dtype, schedule, waves)
- * launches, for profiler kernel filters (cf. KERNEL_NAME in
+ * launches (for G9_SCHED_SPLITK: its segment kernel, followed by
+ * g9_splitk_reduce_f16 or g9_splitk_reduce_bf16 by output type),
+ * for profiler kernel filters (cf. KERNEL_NAME in
  * kernels/gemm/inter_wave/a8w8/matmul_kernel.py:52), or NULL.
  */
 const char* g9_kernel_name(int dtype, int out_dtype, int schedule, int waves);
