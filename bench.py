@@ -537,7 +537,8 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+                                   "(the GEMM shards over output rows with no communication; one GPU's share "
+                                   "is what --gpus 1 measures; nothing multi-GPU is launched)"}))
         sys.exit(2)
     import torch
 
