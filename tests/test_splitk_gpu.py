@@ -215,3 +215,26 @@ def test_splitk_random_shapes_match_dp(gpu, M, N, stages, waves, kind):
     else:
         err = R.rel_frobenius(outs["splitk"].float().cpu().numpy(), dp)
         assert err <= 1e-3, f"relative Frobenius error {err:.3g} against data-parallel"
+
+
+def test_splitk_through_the_drop_in_wrappers(gpu):
+    """schedule="splitk" on the reference-shaped wrappers (4-wave a16w16 `matmul`,
+    8-wave a4w4 `matmul_kernel_only`)."""
+    from gfx950_gluon_tutorials_amd.gemm.inter_wave.a4w4 import matmul_kernel_only as a4w4_8w
+    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as a16w16_4w
+
+    _say("split-K through the wrappers")
+    g = torch.Generator().manual_seed(46)
+    a = (torch.randn(512, 4096, generator=g) * 0.1).half().to(gpu)
+    b = (torch.randn(1024, 4096, generator=g) * 0.1).half().to(gpu)
+    c_sk = a16w16_4w(a, b.T, schedule="splitk")
+    c_dp = a16w16_4w(a, b.T)
+    pa, sa = quant.quantize_mxfp4(torch.randn(300, 2048, generator=g))
+    pb, sb = quant.quantize_mxfp4(torch.randn(520, 2048, generator=g))
+    args = [t.to(gpu) for t in (pa, pb, sa, sb)]
+    f_sk = a4w4_8w(*args, torch.empty(300, 520, dtype=torch.bfloat16, device=gpu), schedule="splitk")
+    torch.cuda.synchronize()
+    _check_f16(c_sk, c_dp.float().cpu().numpy(), 4096, 0.01)
+    ref = R.a4w4_ref(pa.numpy(), pb.numpy(), sa.numpy(), sb.numpy(), "bf16")
+    err = R.rel_frobenius(f_sk.float().cpu().numpy(), ref)
+    assert err <= 1e-3, f"relative Frobenius error {err:.3g}"
