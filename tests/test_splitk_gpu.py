@@ -238,3 +238,22 @@ def test_splitk_through_the_drop_in_wrappers(gpu):
     ref = R.a4w4_ref(pa.numpy(), pb.numpy(), sa.numpy(), sb.numpy(), "bf16")
     err = R.rel_frobenius(f_sk.float().cpu().numpy(), ref)
     assert err <= 1e-3, f"relative Frobenius error {err:.3g}"
+
+
+@pytest.mark.parametrize("pad", [24, 5])
+def test_splitk_strided_c_leaves_the_padding_alone(gpu, pad):
+    """C as a column slice of a wider buffer (row stride N + pad; pad 5 makes rows
+    misaligned for 16-byte stores): split-K writes exactly the M x N window."""
+    M, N, K = 300, 520, 2048
+    _say(f"split-K strided C {M}x{N}x{K} pad={pad}")
+    g = torch.Generator().manual_seed(47)
+    a = (torch.randn(M, K, generator=g) * 0.1).half().to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.1).half().to(gpu)
+    buf = torch.full((M, N + pad), 7.0, dtype=torch.float16, device=gpu)
+    c = buf[:, :N]
+    _launch.gemm_a16w16(a, b.T, c, schedule="splitk")
+    want = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    _launch.gemm_a16w16(a, b.T, want, schedule="dp")
+    torch.cuda.synchronize()
+    assert torch.all(buf[:, N:] == 7.0)
+    _check_f16(c, want.float().cpu().numpy(), K, 0.01)
