@@ -164,16 +164,21 @@ int cu_count() {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Split-K workspace layout: the header, then a flag region as large as the
-// one g9_workspace_init clears for a workspace of this size (the flags of any
-// stream-K launch that fits it), then the partials.  Split-K never writes the
-// header or the flags, so one workspace serves both schedules.
+// Workspace layout (both schedules): the header, then a flag region as large
+// as the one g9_workspace_init clears for a workspace of this size (the flags
+// of any stream-K launch that fits it), then the partials.  Split-K never
+// writes the header or the flags, so one workspace serves both schedules.
 size_t splitk_base(size_t ws_bytes) {
   return kWsHeader + flags_bytes((long long)((ws_bytes - kWsHeader) / kWsTileBytes + 1));
 }
+// Smallest workspace whose partials (behind its own flag region) hold
+// `partials` tiles.  Stream-K needs one partial (and one flag) per tile.
 size_t splitk_bytes(long long partials) {
-  return kWsHeader + flags_bytes(partials + 1) + (size_t)partials * kWsTileBytes;
+  size_t s = kWsHeader + flags_bytes(partials + 1) + (size_t)partials * kWsTileBytes;
+  while (splitk_base(s) + (size_t)partials * kWsTileBytes > s) s += 256;
+  return s;
 }
+size_t streamk_bytes(long long tiles) { return splitk_bytes(tiles); }
 
 // Shared launch path.  Sizes/strides were validated by the caller except the
 // generic checks done here.
@@ -218,12 +223,16 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
   } else if (schedule == G9_SCHED_DP) {
     grid = (int)tiles;
   } else {
-    const size_t need = kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
-    if (!ws || ws_bytes < need || !aligned(ws, 256)) return G9_ERR_WORKSPACE;
+    // The partials go behind the whole flag region g9_workspace_init clears
+    // for this workspace size (as split-K's do), so a launch with fewer tiles
+    // never writes partials over flag words a later, larger launch polls.
+    if (!ws || ws_bytes < streamk_bytes(tiles) || !aligned(ws, 256)) return G9_ERR_WORKSPACE;
+    const size_t base = splitk_base(ws_bytes);
+    if (base + (size_t)tiles * kWsTileBytes > ws_bytes) return G9_ERR_WORKSPACE;
     char* w = static_cast<char*>(ws);
     p.err = reinterpret_cast<int*>(w);
     p.flags = reinterpret_cast<u32*>(w + kWsHeader);
-    p.ws = reinterpret_cast<float*>(w + kWsHeader + flags_bytes(tiles));
+    p.ws = reinterpret_cast<float*>(w + base);
     p.epoch = (g_epoch.fetch_add(1) % 65535u) + 1u;
     const long long units = tiles * p.ns;
     int cus = cu_count();
@@ -295,18 +304,17 @@ int check_operand(const void* p, int64_t row_stride_bytes, int64_t k_stride, int
 
 }  // namespace
 
-extern "C" {
-
-int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
-                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
-                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
-                   void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+// Validates the a16w16 arguments and fills p.
+int prep_a16w16(GemmParams& p, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
+                int64_t stride_cn, int dtype) {
   if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
   int st = check_common(M, N, K, dtype, stride_cm, stride_cn, c);
   if (st) return st;
   if ((st = check_operand(a, stride_am * 2, stride_ak, K * 2))) return st;
   if ((st = check_operand(b, stride_bn * 2, stride_bk, K * 2))) return st;
-  GemmParams p{};
+  p = GemmParams{};
   p.a = static_cast<const char*>(a);
   p.b = static_cast<const char*>(b);
   p.c = static_cast<char*>(c);
@@ -317,6 +325,20 @@ int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, 
   p.ldb = (u32)(stride_bn * 2);
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(dtype));
+  return G9_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  GemmParams p;
+  const int st = prep_a16w16(p, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
+                             dtype);
+  if (st) return st;
   return launch(dtype, dtype, schedule, waves, p, workspace, workspace_bytes, stream);
 }
 
@@ -481,7 +503,7 @@ size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedul
     return S > 1 ? splitk_bytes(tiles * S) : 0;
   }
   if (schedule != G9_SCHED_SK) return 0;
-  return kWsHeader + flags_bytes(tiles) + (size_t)tiles * kWsTileBytes;
+  return streamk_bytes(tiles);
 }
 
 // Split factor from a cost model in units of one K stage (~2048 MFMA cycles):

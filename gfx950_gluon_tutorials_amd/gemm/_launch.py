@@ -13,6 +13,7 @@ what ``kernels/gemm/inter_wave/a8w8/matmul_kernel.py:385`` does unconditionally.
 
 from __future__ import annotations
 
+import os
 import threading
 
 import torch
@@ -76,8 +77,12 @@ def _stream(dev: torch.device) -> int:
 
 
 def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
-    """Returns a (K, N) view whose K stride is 1 (an (N, K) row-major buffer)."""
-    if b_kn.stride(0) == 1 and b_kn.stride(1) >= b_kn.shape[0]:
+    """Returns a (K, N) view whose K stride is 1 and whose N rows start on
+    16-byte boundaries (an (N, K) row-major buffer, as the kernels' LDS-DMA
+    needs); anything else is repacked."""
+    es = b_kn.element_size()
+    if (b_kn.stride(0) == 1 and b_kn.stride(1) >= b_kn.shape[0] and b_kn.data_ptr() % 16 == 0
+            and (b_kn.stride(1) * es) % 16 == 0):
         return b_kn
     return b_kn.t().contiguous().t()
 
@@ -94,46 +99,81 @@ def _rows_ok(t: torch.Tensor) -> bool:
     )
 
 
+def _dev_index(dev: torch.device) -> int:
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
 class _Workspaces:
-    """Per-device stream-K workspace (fp32 partial tiles + flags), grown on
-    demand and zeroed once.  Launches that reuse it are ordered on one stream;
-    launches on different streams must not overlap."""
+    """Stream-K / split-K workspaces (fp32 partial tiles + flags), one per
+    (device, stream), grown on demand and zeroed when (re)allocated.
+
+    A workspace is only ever used by launches on its own stream, which the
+    stream orders, so launches on different streams never share partials or
+    flags.  Each workspace is allocated while its stream is current, so the
+    caching allocator ties the memory to that stream as well."""
 
     def __init__(self):
         self._lock = threading.Lock()
-        self._ws: dict[int, torch.Tensor] = {}
+        self._ws: dict[tuple[int, int], torch.Tensor] = {}
 
     def get(self, dev: torch.device, nbytes: int, stream: int) -> tuple[int, int]:
         if nbytes == 0:
             return 0, 0
-        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        key = (_dev_index(dev), int(stream))
         with self._lock:
-            ws = self._ws.get(idx)
+            ws = self._ws.get(key)
             if ws is None or ws.numel() < nbytes:
                 ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
                 _lib.check(_lib.load().g9_workspace_init(ws.data_ptr(), ws.numel(), stream), "workspace init")
-                self._ws[idx] = ws
+                self._ws[key] = ws
         return ws.data_ptr(), ws.numel()
 
-    def error(self, dev: torch.device) -> int:
-        """Synchronises the device's current stream and returns the error word
-        (1 = a stream-K flag wait timed out)."""
-        idx = dev.index if dev.index is not None else torch.cuda.current_device()
-        ws = self._ws.get(idx)
+    def error(self, dev: torch.device, stream: int | None = None) -> int:
+        """Synchronises `stream` (default: the device's current stream) and
+        returns its workspace's error word (1 = a stream-K flag wait timed
+        out; the output of that launch is wrong)."""
+        s = _stream(dev) if stream is None else int(stream)
+        ws = self._ws.get((_dev_index(dev), s))
         if ws is None:
             return 0
         out = _lib.ctypes.c_int(0)
-        _lib.check(_lib.load().g9_workspace_error(ws.data_ptr(), ws.numel(), _stream(dev), _lib.ctypes.byref(out)),
+        _lib.check(_lib.load().g9_workspace_error(ws.data_ptr(), ws.numel(), s, _lib.ctypes.byref(out)),
                    "workspace error query")
         return out.value
 
+    def check(self, dev: torch.device, stream: int | None = None) -> None:
+        """Raises RuntimeError if a stream-K launch on `stream` timed out in a
+        flag wait, after clearing the workspace so later launches start
+        clean."""
+        err = self.error(dev, stream)
+        if err:
+            s = _stream(dev) if stream is None else int(stream)
+            ws = self._ws[(_dev_index(dev), s)]
+            _lib.check(_lib.load().g9_workspace_init(ws.data_ptr(), ws.numel(), s), "workspace init")
+            raise RuntimeError(f"stream-K flag wait timed out on {dev} (error word {err}); that output is wrong")
+
+    def release(self) -> None:
+        """Drops every cached workspace (their memory returns to torch's
+        caching allocator once the streams that used it are done)."""
+        with self._lock:
+            self._ws.clear()
+
 
 WORKSPACES = _Workspaces()
+
+# G9_CHECK=1: after every stream-K launch, synchronise its stream and raise if
+# a flag wait timed out (a debugging aid: it serialises the host with the GPU).
+CHECK_STREAMK = os.environ.get("G9_CHECK", "0") not in ("", "0")
 
 
 def _workspace(lib, dt: int, M: int, N: int, K: int, sched: int, waves: int, dev, stream) -> tuple[int, int]:
     need = lib.g9_workspace_size(dt, M, N, K, sched, waves)
     return WORKSPACES.get(dev, need, stream)
+
+
+def _after_launch(sched: int, dev, stream: int) -> None:
+    if CHECK_STREAMK and sched == _lib.G9_SCHED_SK:
+        WORKSPACES.check(dev, stream)
 
 
 def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedule="dp", waves: int = 4):
@@ -157,6 +197,7 @@ def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedul
                             a.stride(0), a.stride(1), b_kn.stride(0), b_kn.stride(1),
                             c.stride(0), c.stride(1), dt, sched, waves, ws, ws_bytes, stream)
     _lib.check(rc, "g9_gemm_a16w16")
+    _after_launch(sched, dev, stream)
     return c
 
 
@@ -198,6 +239,7 @@ def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=N
                           sb.data_ptr() if sb is not None else None,
                           _OUT_CODE[c.dtype], sched, waves, ws, ws_bytes, stream)
     _lib.check(rc, "g9_gemm_a8w8")
+    _after_launch(sched, dev, stream)
     return c
 
 
@@ -243,4 +285,5 @@ def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales
                           b_scales.stride(0), b_scales.stride(1), _OUT_CODE[c.dtype], sched, waves,
                           ws, ws_bytes, stream)
     _lib.check(rc, "g9_gemm_a4w4")
+    _after_launch(sched, dev, stream)
     return c

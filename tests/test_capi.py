@@ -108,11 +108,55 @@ def test_splitk_factor_invariants():
                     assert 100 * (-(-stages // s)) + 700 + 4 * s * tiles < 100 * stages + 400
 
 
+def _flags_base(ws_bytes):
+    """Start of the partials in a workspace of ws_bytes: behind the header and
+    the flag words g9_workspace_init clears for that size (one per tile whose
+    partial fits, plus one, rounded up to 256 bytes)."""
+    tile = 256 * 256 * 4
+    max_tiles = (ws_bytes - 256) // tile + 1
+    return 256 + -(-max_tiles * 4 // 256) * 256
+
+
 def test_workspace_size():
     lib = _lib.load()
     assert lib.g9_workspace_size(_lib.G9_F16, 4096, 4096, 8192, _lib.G9_SCHED_DP, 4) == 0
     sk = lib.g9_workspace_size(_lib.G9_F16, 3840, 3840, 16384, _lib.G9_SCHED_SK, 4)
     assert sk >= 225 * 256 * 256 * 4 + 225 * 4
+    # An exact-size workspace holds every tile's partial behind the flag
+    # region its own size implies (tile counts up to and past the point where
+    # the flags outgrow one 256 KiB partial).
+    for M, N in ((256, 256), (3840, 3840), (5120, 5120), (65536, 65536), (65536 + 256, 65536 + 512)):
+        tiles = -(-M // 256) * -(-N // 256)
+        ws = lib.g9_workspace_size(_lib.G9_F16, M, N, 1024, _lib.G9_SCHED_SK, 4)
+        assert _flags_base(ws) + tiles * 256 * 256 * 4 <= ws, (M, N)
+        assert _flags_base(ws) >= 256 + 4 * (tiles + 1)
+
+
+def test_streamk_rejects_a_workspace_256_bytes_short():
+    """Validation only: the call fails before launching (no GPU work)."""
+    lib = _lib.load()
+    M, N, K = 3840, 3840, 1024
+    ws = lib.g9_workspace_size(_lib.G9_F16, M, N, K, _lib.G9_SCHED_SK, 4)
+    short = lib.g9_gemm_a16w16(FAKE, FAKE, FAKE, M, N, K, K, 1, 1, K, N, 1, _lib.G9_F16, _lib.G9_SCHED_SK, 4,
+                               FAKE, ws - 256, None)
+    assert short == _lib.G9_ERR_WORKSPACE
+
+
+def test_b_operand_rows_not_16_byte_aligned_are_repacked():
+    import torch
+
+    from gfx950_gluon_tutorials_amd.gemm import _launch
+
+    buf = torch.zeros(384, 1024 + 4, dtype=torch.float16)
+    for off in (0, 4):
+        b_kn = buf[:, off:off + 1024].T  # (K, N) view with unit K stride
+        got = _launch._k_major(b_kn)
+        assert got.stride(0) == 1 and got.data_ptr() % 16 == 0 and (got.stride(1) * 2) % 16 == 0
+        assert torch.equal(got, b_kn)
+    # Unit K stride but a 1028-element (2056-byte) row pitch: repacked.
+    assert _launch._k_major(buf[:, :1024].T).data_ptr() != buf.data_ptr()
+    aligned = torch.zeros(384, 1024, dtype=torch.float16)
+    assert _launch._k_major(aligned.T).data_ptr() == aligned.data_ptr()  # used in place
 
 
 def _a16w16(M=512, N=512, K=1024, sam=None, sak=1, sbk=1, sbn=None, scm=None, scn=1, dtype=0, sched=0,
