@@ -25,6 +25,7 @@ G9_ERR_DTYPE = 3
 G9_ERR_SCHEDULE = 4
 G9_ERR_WORKSPACE = 5
 G9_ERR_HIP = 6
+G9_ERR_SCRATCH = 7
 
 # Element types.
 G9_F16 = 0
@@ -49,6 +50,8 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "g9_gemm_a16w16": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _int, _int, _int, _vp, _sz, _vp]),
+    "g9_gemm_a16w16_noalloc": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                      _int, _int, _int, _vp]),
     "g9_gemm_a8w8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _vp, _vp, _int, _int, _int, _vp, _sz, _vp]),
     "g9_gemm_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

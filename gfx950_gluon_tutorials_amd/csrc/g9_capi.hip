@@ -3,6 +3,7 @@
 // fills a GemmParams and launches one named kernel on the caller's stream
 // (split-K: the segment kernel, then its reduction, on that stream).
 #include <atomic>
+#include <mutex>
 
 #include "../../include/gfx950_gemm.h"
 #include "g9_gemm.hpp"
@@ -305,7 +306,7 @@ int check_operand(const void* p, int64_t row_stride_bytes, int64_t k_stride, int
 }  // namespace
 
 namespace {
-// Validates the a16w16 arguments and fills p.
+// Validates the a16w16 arguments and fills p (shared by the two a16w16 entry points).
 int prep_a16w16(GemmParams& p, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                 int64_t stride_cn, int dtype) {
@@ -587,11 +588,91 @@ const char* g9_status_string(int status) {
       return "stream-K / split-K workspace missing or too small";
     case G9_ERR_HIP:
       return "HIP launch failed";
+    case G9_ERR_SCRATCH:
+      return "the call needs more workspace than the static scratch buffer of g9_gemm_a16w16_noalloc holds";
   }
   return "unknown status";
 }
 
 int g9_streamk_workgroups(void) { return cu_count(); }
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free a16w16 (g9_gemm_a16w16_noalloc): the stream-K / split-K
+// workspace is this static device array instead of a caller buffer.  It holds
+// kScratchTiles partial tiles (64 MiB plus the header and flag words) and
+// lives, on every GPU the library runs on, until the process ends.  Host code
+// never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+// ---------------------------------------------------------------------------
+constexpr long long kScratchTiles = G9_NOALLOC_MAX_TILES;
+constexpr size_t kScratchBytes =
+    kWsHeader + ((size_t)(kScratchTiles + 1) * 4 + 255) / 256 * 256 + (size_t)kScratchTiles * kWsTileBytes;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device `dev` (looked up on the
+// first call for that device).
+int scratch_ptr(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxScratchDevices) return G9_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return G9_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return G9_OK;
+}
+
+// Makes `dev` current for the lifetime of the object, restoring the previous
+// device afterwards.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    ok = prev == dev || hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (ok && prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+}  // namespace
+
+extern "C" {
+
+int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                           int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                           int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                           void* stream) {
+  GemmParams p;
+  int st = prep_a16w16(p, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype);
+  if (st) return st;
+  if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
+  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK) return G9_ERR_SCHEDULE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int dev = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess) return G9_ERR_HIP;
+  DeviceGuard guard(dev);
+  if (!guard.ok) return G9_ERR_HIP;
+  const size_t need = g9_workspace_size(dtype, M, N, K, schedule, waves);
+  if (need == 0) return launch(dtype, dtype, schedule, waves, p, nullptr, 0, stream);
+  if (need > kScratchBytes) return G9_ERR_SCRATCH;
+  void* ws = nullptr;
+  if ((st = scratch_ptr(dev, &ws))) return st;
+  // Stream-K needs its error word and flags at zero: clear them with a fill
+  // kernel (no hipMemsetAsync, so the call can be captured in a graph).
+  // Split-K writes every partial it reads, so it needs no clearing.
+  if (schedule == G9_SCHED_SK && (st = g9_workspace_init(ws, kScratchBytes, stream))) return st;
+  return launch(dtype, dtype, schedule, waves, p, ws, kScratchBytes, stream);
+}
 
 int g9_version(void) { return 100; }
 

@@ -42,7 +42,8 @@ enum {
   G9_ERR_DTYPE = 3,     /* unsupported element / output type */
   G9_ERR_SCHEDULE = 4,  /* unknown schedule or wave count */
   G9_ERR_WORKSPACE = 5, /* stream-K / split-K workspace missing or too small */
-  G9_ERR_HIP = 6        /* the HIP runtime rejected the launch */
+  G9_ERR_HIP = 6,       /* the HIP runtime rejected the launch */
+  G9_ERR_SCRATCH = 7    /* g9_gemm_a16w16_noalloc: the call needs more than its static scratch buffer */
 };
 
 /* Element / output types. */
@@ -64,6 +65,29 @@ int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, 
                    int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
                    int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of g9_gemm_a16w16, for callers that cannot
+ * allocate device memory or own a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same arguments, kernels and results as g9_gemm_a16w16
+ * without the workspace: the stream-K and split-K partials live in a static
+ * device array of the library (one per GPU, held until the process ends) of
+ * G9_NOALLOC_MAX_TILES fp32 partial tiles of 256 x 256 (64 MiB) plus a header
+ * and flag words.  A call that needs more (stream-K on more tiles, split-K
+ * with more segment tiles) returns G9_ERR_SCRATCH; data-parallel needs none.
+ * The call allocates nothing: a stream-K call first clears the array's flag
+ * and error words with a fill kernel on `stream` (no memset), split-K writes
+ * every partial it reads.  Calls share their GPU's array, so calls that may
+ * overlap on one GPU (other streams, other host threads) race and must be
+ * ordered by the caller.  A stream-K flag wait that times out (only possible
+ * when calls overlap) leaves a wrong output and is not reported.
+ */
+#define G9_NOALLOC_MAX_TILES 256
+int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                           int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                           int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                           void* stream);
 
 /*
  * a8w8: BF8 (fp8 e5m2) in, fp32 accumulate, C = (A.B) * a_scale[0] * b_scale[0]

@@ -51,9 +51,27 @@ def test_timing_build_exports_its_header_and_the_regular_one_does_not():
 def test_version_and_status_strings():
     lib = _lib.load()
     assert lib.g9_version() >= 100
-    for code in range(7):
-        assert _lib.status_text(code)
+    for code in range(8):
+        assert _lib.status_text(code) != "unknown status"
     assert _lib.status_text(0) == "ok"
+    assert "scratch" in _lib.status_text(_lib.G9_ERR_SCRATCH)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=0), _lib.G9_ERR_SHAPE),
+    (dict(K=100), _lib.G9_ERR_SHAPE),
+    (dict(sak=2), _lib.G9_ERR_LAYOUT),
+    (dict(dtype=_lib.G9_BF8), _lib.G9_ERR_DTYPE),
+])
+def test_noalloc_argument_validation(kw, code):
+    """The allocation-free entry validates exactly like g9_gemm_a16w16 (bad
+    arguments only: nothing reaches the device)."""
+    args = dict(M=512, N=512, K=1024, sak=1, dtype=_lib.G9_F16)
+    args.update(kw)
+    M, N, K = args["M"], args["N"], args["K"]
+    lib = _lib.load()
+    assert lib.g9_gemm_a16w16_noalloc(FAKE, FAKE, FAKE, M, N, K, K, args["sak"], 1, K, N, 1, args["dtype"],
+                                      _lib.G9_SCHED_SK, 4, None) == code
 
 
 def test_kernel_names_are_stable_and_unique():
