@@ -32,6 +32,7 @@ G9_F16 = 0
 G9_BF16 = 1
 G9_BF8 = 2
 G9_FP4 = 3
+G9_FP4P = 4  # MXFP4 with preshuffled scales (g9_gemm_a4w4_preshuffled)
 
 # Schedules.
 G9_SCHED_DP = 0
@@ -56,6 +57,8 @@ SIGNATURES = {
                             _vp, _vp, _int, _int, _int, _vp, _sz, _vp]),
     "g9_gemm_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]),
+    "g9_gemm_a4w4_preshuffled": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _i64, _i64, _i64, _int, _int, _int, _vp, _sz, _vp]),
     "g9_moe_a16w16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "g9_moe_a8w8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                            _vp]),

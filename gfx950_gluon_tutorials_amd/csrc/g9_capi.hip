@@ -38,6 +38,15 @@ G9_DEFINE(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
 G9_DEFINE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
 G9_DEFINE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
+// MXFP4 with preshuffled scales: data-parallel, 4-wave.
+using G9Fp4p4 = Geo4<kMfmaDim<Op::FP4P>>;
+extern "C" __global__ G9_ATTRS(G9Fp4p4) void g9_a4w4ps_bf16out_dp_4w(GemmParams p) {
+  gemm_dp<Op::FP4P, OUT_BF16, G9Fp4p4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Fp4p4) void g9_a4w4ps_f16out_dp_4w(GemmParams p) {
+  gemm_dp<Op::FP4P, OUT_F16, G9Fp4p4>(p);
+}
+
 // Grouped (MoE) kernels, 4-wave.
 #define G9_DEFINE_MOE(NAME, OP, OUT)                                                                \
   extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_moe_4w(GemmParams p) {                      \
@@ -90,6 +99,8 @@ const KernelEntry kKernels[] = {
     G9_ENTRY(G9_F16, G9_F16, g9_a16w16_f16),     G9_ENTRY(G9_BF16, G9_BF16, g9_a16w16_bf16),
     G9_ENTRY(G9_BF8, G9_F16, g9_a8w8_f16out),    G9_ENTRY(G9_BF8, G9_BF16, g9_a8w8_bf16out),
     G9_ENTRY(G9_FP4, G9_BF16, g9_a4w4_bf16out),  G9_ENTRY(G9_FP4, G9_F16, g9_a4w4_f16out),
+    {G9_FP4P, G9_BF16, G9_SCHED_DP, 4, g9_a4w4ps_bf16out_dp_4w, "g9_a4w4ps_bf16out_dp_4w"},
+    {G9_FP4P, G9_F16, G9_SCHED_DP, 4, g9_a4w4ps_f16out_dp_4w, "g9_a4w4ps_f16out_dp_4w"},
 };
 
 #define G9_SPLITK_ENTRY(DT, OUT, NAME)                                                              \
@@ -135,6 +146,7 @@ int stage_k(int dtype) {
     case G9_BF8:
       return 128;
     case G9_FP4:
+    case G9_FP4P:
       return 256;
   }
   return 0;
@@ -402,6 +414,47 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(G9_FP4));
   return launch(G9_FP4, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+}
+
+int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                             int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                             int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                             int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
+  int st = check_common(M, N, K, G9_FP4P, stride_cm, stride_cn, c);
+  if (st) return st;
+  if ((st = check_operand(a, stride_am, stride_ak, K / 2))) return st;
+  if ((st = check_operand(b, stride_bn, stride_bk, K / 2))) return st;
+  if (schedule != G9_SCHED_DP || waves != 4) return G9_ERR_SCHEDULE;
+  // Chunks of 32 bytes per row; every chunk part is a 16-byte aligned KiB.
+  if (!a_scales || !b_scales || !aligned(a_scales, 16) || !aligned(b_scales, 16)) return G9_ERR_LAYOUT;
+  const int64_t chunks = (K / 256 + 3) / 4;
+  if (chunks == 1) {  // the stride of a single chunk is never used (and reads as anything in a size-1 dimension)
+    stride_asc = 32 * M;
+    stride_bsc = 32 * N;
+  }
+  if (stride_asc < 32 * M || stride_bsc < 32 * N || stride_asc % 16 || stride_bsc % 16) return G9_ERR_LAYOUT;
+  // The kernel addresses each scale array with 32-bit offsets below 2^31.
+  if ((chunks - 1) * stride_asc + 32 * M + 4096 >= (int64_t(1) << 31) ||
+      (chunks - 1) * stride_bsc + 32 * N + 4096 >= (int64_t(1) << 31))
+    return G9_ERR_SHAPE;
+  GemmParams p{};
+  p.a = static_cast<const char*>(a);
+  p.b = static_cast<const char*>(b);
+  p.c = static_cast<char*>(c);
+  p.a_sc = static_cast<const unsigned char*>(a_scales);
+  p.b_sc = static_cast<const unsigned char*>(b_scales);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.lda = (u32)stride_am;
+  p.ldb = (u32)stride_bn;
+  p.ldsa = (u32)stride_asc;
+  p.ldsb = (u32)stride_bsc;
+  p.ldc = stride_cm;
+  p.ns = (int)(K / stage_k(G9_FP4P));
+  return launch(G9_FP4P, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
 }
 
 int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_offsets, int64_t T,

@@ -113,7 +113,10 @@ G9_DEV void sk_stamp(int) {}
 G9_DEV void sk_times_store(const SkTimes&) {}
 #endif
 
-enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3 };
+// FP4P: MXFP4 with preshuffled E8M0 scales (see Pipe::init): the same data
+// and MFMAs as FP4, but each lane's scale bytes for four stages arrive with
+// one LDS read and no byte permute.
+enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3, FP4P = 4 };
 enum : int { OUT_F16 = 0, OUT_BF16 = 1 };
 
 struct GemmParams {
@@ -238,11 +241,12 @@ struct Frag {
 
 template <Op OP>
 struct OpInfo {
-  static constexpr bool kScaled = OP == Op::FP4;
+  static constexpr bool kScaled = OP == Op::FP4 || OP == Op::FP4P;
+  static constexpr bool kPreshuffled = OP == Op::FP4P;
   static constexpr int kChunksPerMfma = OP == Op::BF8 ? 2 : 1;  // 16-byte chunks per lane per MFMA
 };
 template <Op OP>
-constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : G9_MD_F16;
+constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : OP == Op::FP4P ? 16 : G9_MD_F16;
 // The 8-wave MXFP4 kernel uses 32x32x64 fragments: with 16x16 ones its
 // operand sets, scale bytes and DMA offsets exceed the 128 VGPRs a wave has
 // beside its accumulators at 2 waves per SIMD, and the spill reloads inside
@@ -251,7 +255,7 @@ constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 :
 #define G9_MD_FP4_8W 32
 #endif
 template <Op OP>
-constexpr int kMfmaDim8 = OP == Op::FP4 ? G9_MD_FP4_8W : kMfmaDim<OP>;
+constexpr int kMfmaDim8 = OP == Op::FP4 || OP == Op::FP4P ? G9_MD_FP4_8W : kMfmaDim<OP>;
 
 // Per-region work and the DMA pattern of the main loop.  The loop body covers
 // kBody stages = 4 * kBody regions, numbered by their body position.  Every
@@ -319,29 +323,37 @@ G9_DEV V load_quads(const f32x4* p) {
 // LDS byte offset of operand sub-buffer X (0:A0 1:A1 2:B0 3:B1) in slot s.
 constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s) * kSubBytes; }
 
-// Block-scaled MFMA step E: byte E of each scale VGPR is the scale
-// (op_sel and op_sel_hi bit 0 of the scale operands select the byte).
-#define G9_MFMA_SCALED(SHAPE)                                                                          \
-  do {                                                                                                 \
-    if constexpr (E == 0)                                                                              \
-      asm("v_mfma_scale_f32_" SHAPE "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"   \
-          : "+a"(acc)                                                                                  \
-          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
-    else if constexpr (E == 1)                                                                         \
-      asm("v_mfma_scale_f32_" SHAPE                                                                    \
-          "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[0,0,0] cbsz:4 blgp:4"              \
-          : "+a"(acc)                                                                                  \
-          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
-    else if constexpr (E == 2)                                                                         \
-      asm("v_mfma_scale_f32_" SHAPE "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,1,0] cbsz:4 blgp:4"   \
-          : "+a"(acc)                                                                                  \
-          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
-    else                                                                                               \
-      asm("v_mfma_scale_f32_" SHAPE                                                                    \
-          "_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,1,0] op_sel_hi:[1,1,0] cbsz:4 blgp:4"              \
-          : "+a"(acc)                                                                                  \
-          : "v"(bx.c[E]), "v"(ay.c[E]), "v"(bx.sp), "v"(ay.sp));                                      \
-  } while (0)
+// Block-scaled e2m1 x e2m1 MFMA (format code 4) whose scales are byte BYTE of
+// sx (for x, the MFMA's first operand) and of sy: op_sel and op_sel_hi bit 0
+// of the scale operands select the byte.
+#define G9_MFMA_SCALED_ASM(SHAPE, SEL)                                                               \
+  asm("v_mfma_scale_f32_" SHAPE "_f8f6f4 %0, %1, %2, %0, %3, %4 " SEL " cbsz:4 blgp:4"              \
+      : "+a"(acc)                                                                                 \
+      : "v"(x), "v"(y), "v"(sx), "v"(sy))
+template <int BYTE, class ACC>
+G9_DEV void mfma_scaled(ACC& acc, const u32x4& x, const u32x4& y, u32 sx, u32 sy) {
+  static_assert(BYTE >= 0 && BYTE < 4, "a scale VGPR holds four bytes");
+  if constexpr (sizeof(ACC) == sizeof(f32x4)) {
+    if constexpr (BYTE == 0)
+      G9_MFMA_SCALED_ASM("16x16x128", "op_sel_hi:[0,0,0]");
+    else if constexpr (BYTE == 1)
+      G9_MFMA_SCALED_ASM("16x16x128", "op_sel:[1,1,0] op_sel_hi:[0,0,0]");
+    else if constexpr (BYTE == 2)
+      G9_MFMA_SCALED_ASM("16x16x128", "op_sel_hi:[1,1,0]");
+    else
+      G9_MFMA_SCALED_ASM("16x16x128", "op_sel:[1,1,0] op_sel_hi:[1,1,0]");
+  } else {
+    if constexpr (BYTE == 0)
+      G9_MFMA_SCALED_ASM("32x32x64", "op_sel_hi:[0,0,0]");
+    else if constexpr (BYTE == 1)
+      G9_MFMA_SCALED_ASM("32x32x64", "op_sel:[1,1,0] op_sel_hi:[0,0,0]");
+    else if constexpr (BYTE == 2)
+      G9_MFMA_SCALED_ASM("32x32x64", "op_sel_hi:[1,1,0]");
+    else
+      G9_MFMA_SCALED_ASM("32x32x64", "op_sel:[1,1,0] op_sel_hi:[1,1,0]");
+  }
+}
+#undef G9_MFMA_SCALED_ASM
 
 // MFMA step E of the stage on a (B fragment, A fragment) pair, written as
 // inline assembly with the accumulator tied in place ("+a").  The compiler
@@ -354,6 +366,7 @@ constexpr int sub_off(int X, int s) { return (X >> 1) * 65536 + ((X & 1) * 2 + s
 // MFMAs accumulating into the same registers need no wait states.)
 template <Op OP, class G, int E>
 G9_DEV void mma(accv<G>& acc, const Frag<G::NC>& bx, const Frag<G::NC>& ay) {
+  static_assert(OP != Op::FP4P, "preshuffled-scale MFMAs take their scales from ScRegs");
   if constexpr (G::MD == 16) {
     if constexpr (OP == Op::F16) {
       asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bx.c[E]), "v"(ay.c[E]));
@@ -366,8 +379,8 @@ G9_DEV void mma(accv<G>& acc, const Frag<G::NC>& bx, const Frag<G::NC>& ay) {
       const i32x8 y = __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[0], ay.c[1], 0, 1, 2, 3, 4, 5, 6, 7));
       asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
     } else {
-      // e2m1 x e2m1 (format code 4), 16 bytes per lane.
-      G9_MFMA_SCALED("16x16x128");
+      // e2m1 x e2m1, 16 bytes per lane; step E's scales are byte E of sp.
+      mfma_scaled<E>(acc, bx.c[E], ay.c[E], bx.sp, ay.sp);
     }
   } else {
     if constexpr (OP == Op::F16) {
@@ -381,7 +394,7 @@ G9_DEV void mma(accv<G>& acc, const Frag<G::NC>& bx, const Frag<G::NC>& ay) {
           __builtin_bit_cast(i32x8, __builtin_shufflevector(ay.c[2 * E], ay.c[2 * E + 1], 0, 1, 2, 3, 4, 5, 6, 7));
       asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(acc) : "v"(x), "v"(y));
     } else {
-      G9_MFMA_SCALED("32x32x64");
+      mfma_scaled<E>(acc, bx.c[E], ay.c[E], bx.sp, ay.sp);
     }
   }
 }
@@ -431,7 +444,8 @@ struct Slots {
   static constexpr int perm_q(int F) { return NQ - NF - 1 + F; }
   static_assert(NQ >= 1, "a region needs an MFMA after its barrier");
   static_assert(!OpInfo<OP>::kScaled || scale_q(NF - 1) < NQ, "scale reads must fit the region");
-  static_assert(!OpInfo<OP>::kScaled || G::MD != 16 || perm_q(0) >= kLastQ, "permutes must follow the scale reads");
+  static_assert(!OpInfo<OP>::kScaled || OpInfo<OP>::kPreshuffled || G::MD != 16 || perm_q(0) >= kLastQ,
+                "permutes must follow the scale reads");
 };
 
 // Keeps a value in a register the compiler cannot see through, so constant
@@ -454,6 +468,23 @@ G9_DEV u32 opaque_s(u32 x) {
 // traffic) and the sum does not wrap.
 constexpr u32 kDeadOff = 0x80000000u;
 
+// FP4P: a wave's E8M0 scales of one chunk (four stages), one u32x2 per
+// fragment: .x holds stages 0-1 and .y stages 2-3, byte 2 * (stage & 1) + step
+// of each.  A fragment set's scales are read when the region that reads its
+// operands reaches the chunk's first stage.  B0 is used in a stage's first
+// and last regions, so its last use in one chunk and its first in the next
+// are adjacent regions; its registers alternate by chunk parity.  The other
+// sets have two regions between those uses and are overwritten in place.
+template <Op OP, class G>
+struct ScRegs {};
+template <class G>
+struct ScRegs<Op::FP4P, G> {
+  static_assert(G::MD == 16, "preshuffled scales are read for 16x16 fragments");
+  u32x2 a[2][G::FM];   // A0, A1
+  u32x2 b1[G::FN];
+  u32x2 b0[2][G::FN];  // B0, by chunk parity
+};
+
 // Per-workgroup pipeline state: buffer resources, per-lane DMA offsets and LDS
 // read bases.  One instance per output tile (rebuilt per stream-K segment).
 template <Op OP, class G>
@@ -468,6 +499,7 @@ struct Pipe {
   u32 bA[G::NC], bB[G::NC];  // LDS read bases of the lane's chunks (A at 0, B at 64 KiB)
   u32 bS[2][2];             // FP4: LDS read bases [A/B][stages 0-1 / 2-3 of a chunk]
   u32 sel;                  // FP4, MD 16: scale byte selector
+  u32 cstride;              // FP4P: bytes between consecutive scale chunks of this wave's operand
   u32 lds0;                 // LDS address of the shared buffer
   u32 mrow;                 // LDS address of the wave's rows in sub-buffer A0, slot 0
   u32 msc;                  // FP4: LDS address of the wave's chunk rows in chunk slot 0
@@ -522,7 +554,33 @@ struct Pipe {
       bA[c] = opaque(lds0 + (u32)(wm * G::FM * G::MD + rr) * kRowBytes + slot * 16);
       bB[c] = opaque(lds0 + 65536u + (u32)(wn * G::FN * G::MD + rr) * kRowBytes + slot * 16);
     }
-    if constexpr (I::kScaled) {
+    if constexpr (I::kPreshuffled) {
+      // Preshuffled scales (quant.preshuffle_e8m0): chunk c (stages 4c..4c+3)
+      // of row r is 32 bytes at c * cstride + r * 32, byte 8g + 2st + h being
+      // the scale of group 8st + 4h + g (lane group g, stage st of the chunk,
+      // MFMA step h).  A chunk part of 32 rows is one contiguous KiB, so every
+      // part DMA shares one offset and moves by 1024 bytes through its
+      // immediate, in global memory and LDS alike.  The resource covers the
+      // operand's whole scale array; rows past the end in the last chunk read
+      // zero, rows past the end in earlier chunks read the next chunk's rows
+      // (they only meet A or B rows that read zero and outputs that are not
+      // stored).  The LDS chunk slot holds the tile's 512 rows of 32 bytes in
+      // the same order, and lane (row, g) reads its 8 bytes at row * 32 + 8g:
+      // a fragment's 16 rows are 512 contiguous bytes, free of bank conflicts.
+      const int xw = wave / (G::NW / 4);
+      const int r0 = (wave % (G::NW / 4)) * G::kScRows;
+      const bool sa = xw < 2;
+      cstride = __builtin_amdgcn_readfirstlane(sa ? p.ldsa : p.ldsb);
+      const int rows = sa ? p.M : p.N;
+      const u32 nchunks = (u32)(p.ns + kScChunk - 1) / kScChunk;
+      rS = make_rsrc(sa ? p.a_sc : p.b_sc, (nchunks - 1) * cstride + (u32)rows * kScRowBytes);
+      const int hrow = (sa ? tm : tn) * kTile + (xw & 1) * 128;
+      vS[0] = (u32)(hrow + r0) * kScRowBytes + 16u * lane;
+      msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
+      bS[0][0] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + 8 * gi);
+      bS[1][0] = opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 8 * gi);
+      sel = 0;
+    } else if constexpr (I::kScaled) {
       // The wave loads chunk rows [xw * 128 + r0, + kScRows) of the 512: half
       // tile xw (0: A0, 1: A1, 2: B0, 3: B1), rows r0.. of it.  Part j covers
       // 32 of them, two lanes per row; lane l fetches the 16-byte half that
@@ -566,8 +624,14 @@ struct Pipe {
   G9_DEV rsrc_t src(int X) const { return X < 2 ? rA[X & 1] : rB[X & 1]; }
   // SGPR offset of stage `stage` in an operand row (kDeadOff past the end).
   G9_DEV u32 stage_off(int stage) const { return stage < s_end ? (u32)stage * kRowBytes : kDeadOff; }
-  // SGPR offset of the chunk starting at stage `stage` in a scale row.
-  G9_DEV u32 chunk_off(int stage) const { return stage < s_end ? (u32)stage * 8 : kDeadOff; }
+  // SGPR offset of the chunk starting at stage `stage`: in a scale row, or
+  // (FP4P) the chunk's offset in the scale array (stage is a multiple of 4).
+  G9_DEV u32 chunk_off(int stage) const {
+    if constexpr (I::kPreshuffled)
+      return stage < s_end ? (u32)(stage / kScChunk) * cstride : kDeadOff;
+    else
+      return stage < s_end ? (u32)stage * 8 : kDeadOff;
+  }
 
   // 16-byte DMA number J (rows 8J..8J+7 of the wave's kDmaRows) of sub-buffer X.
   // `mb` is mrow, passed through opaque_s once per region: the 8 distinct
@@ -582,8 +646,13 @@ struct Pipe {
   // Part J of the scale chunk whose rows start at `soff` bytes, into chunk slot SSLOT.
   template <int SSLOT, int J>
   G9_DEV void dma_chunk(u32 soff, u32 mb) const {
-    const u32 dst = mb + SSLOT * kScSlotBytes + J * 1024;
-    dma16(rS, (G9_LDS void*)(uintptr_t)dst, vS[J], soff);
+    if constexpr (I::kPreshuffled) {
+      const u32 dst = mb + SSLOT * kScSlotBytes;
+      dma16<J * 1024>(rS, (G9_LDS void*)(uintptr_t)dst, vS[0], soff);
+    } else {
+      const u32 dst = mb + SSLOT * kScSlotBytes + J * 1024;
+      dma16(rS, (G9_LDS void*)(uintptr_t)dst, vS[J], soff);
+    }
   }
 
   // 16-byte LDS read number R (fragment R / NC, chunk R % NC) of sub-buffer X.
@@ -614,6 +683,22 @@ struct Pipe {
       f[F].sp = *(const G9_LDS u32*)(uintptr_t)(base + imm);
   }
 
+  // FP4P: the chunk's scales of every fragment of sub-buffer X from chunk
+  // slot SSLOT (B0 into its registers of chunk parity PAR).
+  template <int X, int SSLOT, int PAR, int F>
+  G9_DEV void read_scales_ps(ScRegs<OP, G>& sr) const {
+    constexpr int imm = SSLOT * kScSlotBytes + (X & 1) * 128 * kScRowBytes + F * G::MD * kScRowBytes;
+    const u32x2 v = *(const G9_LDS u32x2*)(uintptr_t)(bS[X >= 2][0] + imm);
+    if constexpr (X == 0)
+      sr.a[0][F] = v;
+    else if constexpr (X == 1)
+      sr.a[1][F] = v;
+    else if constexpr (X == 2)
+      sr.b0[PAR][F] = v;
+    else
+      sr.b1[F] = v;
+  }
+
   // Whole-set variants for the prologue.
   template <int X, int SLOT>
   G9_DEV void issue(int stage) const {
@@ -631,7 +716,7 @@ struct Pipe {
     constexpr int NF = X < 2 ? G::FM : G::FN;
     [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
         std::make_integer_sequence<int, G::NC * NF>{});
-    if constexpr (I::kScaled) {
+    if constexpr (I::kScaled && !I::kPreshuffled) {
       [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SSLOT, ST, F>(f), ...); }(
           std::make_integer_sequence<int, NF>{});
     }
@@ -687,7 +772,7 @@ G9_DEV void settle_acc(Acc<G>& acc) {
 // instruction-class masks do not cover, so only a full fence pins the order).
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS, int K>
 G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u32 mb, u32 ms, QAcc<G>& acc,
-                        const FragSet<G>& bx, const FragSet<G>& ay, FragSet<G>& nxt) {
+                        ScRegs<OP, G>& sr, const FragSet<G>& bx, const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
   using Sh = Shape<OP, G>;
@@ -707,13 +792,31 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
   // (measured: about 0.8% less time for every dtype, identical results).
   constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j0 = K % G::FN;
   constexpr int j = (i % 2) ? G::FN - 1 - j0 : j0;
-  mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
+  if constexpr (OpInfo<OP>::kPreshuffled) {
+    // Region POS % 4 is quadrant (A0,B0), (A0,B1), (A1,B1), (A1,B0); its
+    // stage is stage POS / 4 % 4 of chunk POS / 16 of the body.
+    constexpr int quad = POS % 4, st = (POS / 4) % kScChunk, cp = (POS / 16) % 2;
+    const u32x2& sa = sr.a[quad >= 2 ? 1 : 0][i];
+    const u32x2& sb = (quad == 1 || quad == 2) ? sr.b1[j] : sr.b0[cp][j];
+    mfma_scaled<2 * (st & 1) + e>(acc[i][j], bx[j].c[e], ay[i].c[e], (st >> 1) ? sb.y : sb.x,
+                                  (st >> 1) ? sa.y : sa.x);
+  } else {
+    mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
+  }
   constexpr int q = K - S::kPre;
   if constexpr (q >= 0) {
     static_for<S::NR>([&](auto R) {
       if constexpr (S::read_q(decltype(R)::value) == q) P.template read_chunk<RX, RSLOT, decltype(R)::value>(nxt);
     });
-    if constexpr (OpInfo<OP>::kScaled) {
+    if constexpr (OpInfo<OP>::kPreshuffled) {
+      // The chunk's scales of set RX, when RX is read for a chunk's first stage.
+      if constexpr (kSt == 0) {
+        static_for<NF>([&](auto F) {
+          if constexpr (S::scale_q(decltype(F)::value) == q)
+            P.template read_scales_ps<RX, kSSlot, (ks / kScChunk) % 2, decltype(F)::value>(sr);
+        });
+      }
+    } else if constexpr (OpInfo<OP>::kScaled) {
       static_for<NF>([&](auto F) {
         if constexpr (S::scale_q(decltype(F)::value) == q)
           P.template read_scales<RX, kSSlot, kSt, decltype(F)::value>(nxt);
@@ -723,7 +826,7 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
       if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
     });
     if constexpr (part >= 0 && q == S::kScaleDmaQ) P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, ms);
-    if constexpr (OpInfo<OP>::kScaled && G::MD == 16) {
+    if constexpr (OpInfo<OP>::kScaled && !OpInfo<OP>::kPreshuffled && G::MD == 16) {
       static_for<NF>([&](auto F) {
         constexpr int f = decltype(F)::value;
         if constexpr (S::perm_q(f) == q) {
@@ -748,8 +851,8 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS>
-G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
-                   FragSet<G>& nxt) {
+G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP, G>& sr, const FragSet<G>& bx,
+                   const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
   using Sh = Shape<OP, G>;
@@ -764,11 +867,12 @@ G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, const Frag
     ms = opaque_s(P.msc);
   }
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K>(P, r, soff, soff_sc, mb, ms, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K>(P, r, soff, soff_sc, mb, ms, acc, sr, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::kPre>{});
   barrier();
   [&]<int... K>(std::integer_sequence<int, K...>) {
-    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K + S::kPre>(P, r, soff, soff_sc, mb, ms, acc, bx, ay, nxt), ...);
+    (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K + S::kPre>(P, r, soff, soff_sc, mb, ms, acc, sr, bx, ay, nxt),
+     ...);
   }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
@@ -777,30 +881,30 @@ G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, const Frag
 // stage's B0 fragments go to y as well.  Odd stages (slot 1): B0 in y; B1 to
 // x, then the next stage's B0.
 template <Op OP, class G, int K>
-G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
-                  FragSet<G>& y) {
+G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, ScRegs<OP, G>& sr, FragSet<G>& at, FragSet<G>& ab,
+                  FragSet<G>& x, FragSet<G>& y) {
   constexpr int POS = 4 * K;
   if constexpr (K % 2 == 0) {
-    region<OP, G, 3, 0, 2, 0, POS + 0>(P, s, s + K + 2, acc[0][0], x, at, y);
-    region<OP, G, 1, 0, 3, 0, POS + 1>(P, s, s + K + 2, acc[0][1], y, at, ab);
-    region<OP, G, 0, 1, 1, 0, POS + 2>(P, s, s + K + 2, acc[1][1], y, ab, at);
-    region<OP, G, 2, 1, 0, 1, POS + 3>(P, s, s + K + 3, acc[1][0], x, ab, y);
+    region<OP, G, 3, 0, 2, 0, POS + 0>(P, s, s + K + 2, acc[0][0], sr, x, at, y);
+    region<OP, G, 1, 0, 3, 0, POS + 1>(P, s, s + K + 2, acc[0][1], sr, y, at, ab);
+    region<OP, G, 0, 1, 1, 0, POS + 2>(P, s, s + K + 2, acc[1][1], sr, y, ab, at);
+    region<OP, G, 2, 1, 0, 1, POS + 3>(P, s, s + K + 3, acc[1][0], sr, x, ab, y);
   } else {
-    region<OP, G, 3, 1, 2, 1, POS + 0>(P, s, s + K + 2, acc[0][0], y, at, x);
-    region<OP, G, 1, 1, 3, 1, POS + 1>(P, s, s + K + 2, acc[0][1], x, at, ab);
-    region<OP, G, 0, 0, 1, 1, POS + 2>(P, s, s + K + 2, acc[1][1], x, ab, at);
-    region<OP, G, 2, 0, 0, 0, POS + 3>(P, s, s + K + 3, acc[1][0], y, ab, x);
+    region<OP, G, 3, 1, 2, 1, POS + 0>(P, s, s + K + 2, acc[0][0], sr, y, at, x);
+    region<OP, G, 1, 1, 3, 1, POS + 1>(P, s, s + K + 2, acc[0][1], sr, x, at, ab);
+    region<OP, G, 0, 0, 1, 1, POS + 2>(P, s, s + K + 2, acc[1][1], sr, x, ab, at);
+    region<OP, G, 2, 0, 0, 0, POS + 3>(P, s, s + K + 3, acc[1][0], sr, y, ab, x);
   }
 }
 
 // The last n < kBody stages (a partial body): stages 0 .. n-1.
 template <Op OP, class G, int K>
-G9_DEV void tail(const Pipe<OP, G>& P, int s, int n, Acc<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
-                 FragSet<G>& y) {
+G9_DEV void tail(const Pipe<OP, G>& P, int s, int n, Acc<G>& acc, ScRegs<OP, G>& sr, FragSet<G>& at, FragSet<G>& ab,
+                 FragSet<G>& x, FragSet<G>& y) {
   if constexpr (K + 1 < Shape<OP, G>::kBody) {
     if (n > K) {
-      stage<OP, G, K>(P, s, acc, at, ab, x, y);
-      tail<OP, G, K + 1>(P, s, n, acc, at, ab, x, y);
+      stage<OP, G, K>(P, s, acc, sr, at, ab, x, y);
+      tail<OP, G, K + 1>(P, s, n, acc, sr, at, ab, x, y);
     }
   }
 }
@@ -834,10 +938,17 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   waitcnt<kFirst, 0>();
   barrier();
   FragSet<G> at, ab, x, y;
+  ScRegs<OP, G> sr;
   P.template load<0, 0, 0, 0>(at);
   P.template load<2, 0, 0, 0>(x);
+  if constexpr (OpInfo<OP>::kPreshuffled) {
+    // Chunk 0's scales of A0 and B0 (read by body positions -2 and -1 in the
+    // steady state); B1's and A1's follow in the first two regions.
+    static_for<G::FM>([&](auto F) { P.template read_scales_ps<0, 0, 0, decltype(F)::value>(sr); });
+    static_for<G::FN>([&](auto F) { P.template read_scales_ps<2, 0, 0, decltype(F)::value>(sr); });
+  }
   waitcnt<kFirst, 0>();
-  if constexpr (kScaled && G::MD == 16) {
+  if constexpr (kScaled && !OpInfo<OP>::kPreshuffled && G::MD == 16) {
     P.template gather_scales<0>(at);
     P.template gather_scales<2>(x);
   }
@@ -851,10 +962,10 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   if (stamp) timing_stamp(1);
   int s = s0;
   for (; s + Sh::kBody <= s1; s += Sh::kBody)
-    static_for<Sh::kBody>([&](auto K) { stage<OP, G, decltype(K)::value>(P, s, acc, at, ab, x, y); });
+    static_for<Sh::kBody>([&](auto K) { stage<OP, G, decltype(K)::value>(P, s, acc, sr, at, ab, x, y); });
   settle_acc<G>(acc);
   if (s < s1) {
-    tail<OP, G, 0>(P, s, s1 - s, acc, at, ab, x, y);
+    tail<OP, G, 0>(P, s, s1 - s, acc, sr, at, ab, x, y);
     settle_acc<G>(acc);
   }
   waitcnt<0, 0>();

@@ -247,31 +247,62 @@ def _scales_ok(s: torch.Tensor) -> bool:
     return s.stride(1) == 1 and s.stride(0) % 4 == 0 and s.stride(0) >= s.shape[1] and s.data_ptr() % 4 == 0
 
 
+def _ps_scales_ok(s: torch.Tensor) -> bool:
+    return s.stride(2) == 1 and s.stride(1) == 32 and s.stride(0) % 16 == 0 and s.data_ptr() % 16 == 0
+
+
+def _gemm_a4w4_preshuffled(lib, dev, a, b, a_scales, b_scales, c, M, N, K, schedule, waves):
+    chunks = -(-K // 1024)
+    if a_scales.shape != (chunks, M, 32) or b_scales.shape != (chunks, N, 32):
+        raise ValueError(f"preshuffled scales must be ({chunks}, {M}, 32) and ({chunks}, {N}, 32); got "
+                         f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
+    if not _ps_scales_ok(a_scales):
+        a_scales = a_scales.contiguous()
+    if not _ps_scales_ok(b_scales):
+        b_scales = b_scales.contiguous()
+    sched = _schedule_code(schedule, M, N, _lib.G9_FP4)
+    if sched != _lib.G9_SCHED_DP or waves != 4:
+        raise ValueError("preshuffled MXFP4 scales run on the 4-wave data-parallel kernel only")
+    stream = _stream(dev)
+    rc = lib.g9_gemm_a4w4_preshuffled(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(),
+                                      b_scales.data_ptr(), M, N, K, a.stride(0), a.stride(1), b.stride(0),
+                                      b.stride(1), c.stride(0), c.stride(1), a_scales.stride(0),
+                                      b_scales.stride(0), _OUT_CODE[c.dtype], sched, waves, None, 0, stream)
+    _lib.check(rc, "g9_gemm_a4w4_preshuffled")
+    return c
+
+
 def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales: torch.Tensor, c: torch.Tensor,
               *, schedule="dp", waves: int = 4):
     """C = dequant(A) @ dequant(B)^T with packed MXFP4 A (M, K/2), B (N, K/2)
-    and E8M0 scales (M, K/32), (N, K/32)."""
+    and E8M0 scales (M, K/32), (N, K/32), or both in the preshuffled layout
+    of quant.preshuffle_e8m0 ((ceil(K/1024), M, 32), (ceil(K/1024), N, 32);
+    4-wave data-parallel kernel)."""
     lib = _lib.load()
     dev = _require_device(a, b, a_scales, b_scales, c)
+    preshuffled = a_scales.dim() == 3
     for name, t in (("a", a), ("b", b), ("a_scales", a_scales), ("b_scales", b_scales)):
-        if t.dtype != torch.uint8 or t.dim() != 2:
-            raise ValueError(f"a4w4 {name} must be a 2-D uint8 tensor, got {t.dtype} {tuple(t.shape)}")
-    if c.dtype not in _OUT_CODE:
-        raise ValueError(f"a4w4 output must be bf16 or fp16, got {c.dtype}")
+        want = 3 if preshuffled and name.endswith("scales") else 2
+        if t.dtype != torch.uint8 or t.dim() != want:
+            raise ValueError(f"a4w4 {name} must be a {want}-D uint8 tensor, got {t.dtype} {tuple(t.shape)}")
     M, Kp = a.shape
     N = b.shape[0]
     K = 2 * Kp
     if b.shape[1] != Kp:
         raise ValueError(f"a and b packed K differ: {Kp} vs {b.shape[1]}")
-    if a_scales.shape != (M, K // 32) or b_scales.shape != (N, K // 32):
-        raise ValueError(f"scales must be ({M}, {K // 32}) and ({N}, {K // 32}); got "
-                         f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
+    if c.dtype not in _OUT_CODE:
+        raise ValueError(f"a4w4 output must be bf16 or fp16, got {c.dtype}")
     if c.shape != (M, N):
         raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
     if not _rows_ok(a):
         a = a.contiguous()
     if not _rows_ok(b):
         b = b.contiguous()
+    if preshuffled:
+        return _gemm_a4w4_preshuffled(lib, dev, a, b, a_scales, b_scales, c, M, N, K, schedule, waves)
+    if a_scales.shape != (M, K // 32) or b_scales.shape != (N, K // 32):
+        raise ValueError(f"scales must be ({M}, {K // 32}) and ({N}, {K // 32}); got "
+                         f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
     if not _scales_ok(a_scales):
         a_scales = a_scales.contiguous()
     if not _scales_ok(b_scales):

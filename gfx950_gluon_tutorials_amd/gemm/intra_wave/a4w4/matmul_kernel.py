@@ -4,7 +4,9 @@ Replaces ``matmul(a, b, a_scales, b_scales)`` of
 kernels/gemm/intra_wave/a4w4/v1_sliceMN/matmul_kernel.py:696-742:
 ``a`` (M, K/2) and ``b`` (N, K/2) uint8 with two e2m1 values per byte (low
 nibble = even k), ``a_scales`` (M, K/32) and ``b_scales`` (N, K/32) uint8 E8M0
-(any strides; non-row-major views are repacked), bf16 output.
+(any strides; non-row-major views are repacked), bf16 output.  Scales already
+in the preshuffled layout of ``quant.preshuffle_e8m0`` (3-D tensors) run the
+preshuffled-scale kernel; its results are bit-identical.
 """
 
 import torch

@@ -45,7 +45,7 @@ import sys
 import numpy as np
 
 CYCLES_PER_STAGE = 2048
-STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256}
+STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256, "mxfp4ps": 256}
 REALTIME_HZ = 100e6
 NUM_XCDS = 8
 
@@ -109,6 +109,8 @@ def _inputs(dtype: str, M: int, N: int, K: int, dev, seed: int = 0):
         return qa, qb.T, torch.empty(M, N, dtype=torch.bfloat16, device=dev), sa, sb
     pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=g).to(dev))
     pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=g).to(dev))
+    if dtype == "mxfp4ps":  # preshuffled scales (g9_gemm_a4w4_preshuffled)
+        sa, sb = quant.preshuffle_e8m0(sa), quant.preshuffle_e8m0(sb)
     return pa, pb, sa, sb, torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
 

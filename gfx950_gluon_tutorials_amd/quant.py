@@ -13,6 +13,10 @@ the BF8 and MXFP4 benchmark configurations:
   largest e2m1 exponent), code ``E + 127`` (0 for an all-zero group),
   elements ``RNE(x / 2^E)`` to e2m1 saturated at +-6 with the sign kept,
   packed two per byte with the even k in the low nibble.
+* ``preshuffle_e8m0(scales)``: the MXFP4 scales in the read order of the
+  preshuffled-scale kernel (``g9_gemm_a4w4_preshuffled``): chunk-major, 32
+  bytes per row per chunk of 32 K groups (1024 K values), byte 8g + 2s + h of a
+  chunk row holding group 8s + 4h + g.
 """
 
 from __future__ import annotations
@@ -73,3 +77,40 @@ def dequantize_mxfp4(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor
     s = torch.pow(2.0, scales.float() - 127.0)
     s = torch.where(scales == 255, torch.full_like(s, float("nan")), s)
     return vals * s.repeat_interleave(SCALE_GROUP, dim=1)
+
+
+# Chunks of the preshuffled scale layout: 32 K groups (4 K stages of 256 values).
+PS_CHUNK_GROUPS = 32
+
+
+def _ps_group_order(device=None) -> torch.Tensor:
+    """Position j of a preshuffled chunk row holds group order[j] of the chunk:
+    j = 8g + 2s + h  <->  group 8s + 4h + g."""
+    j = torch.arange(PS_CHUNK_GROUPS, device=device)
+    g, s, h = j // 8, (j % 8) // 2, j % 2
+    return 8 * s + 4 * h + g
+
+
+def preshuffle_e8m0(scales: torch.Tensor) -> torch.Tensor:
+    """(R, K/32) uint8 E8M0 scales -> (ceil(K/1024), R, 32) uint8 in the read
+    order of g9_gemm_a4w4_preshuffled (chunk stride 32 * R bytes).  Groups
+    past K/32 in the last chunk are filled with 127 (scale 1.0); the kernel
+    never uses them."""
+    if scales.dim() != 2 or scales.dtype != torch.uint8:
+        raise ValueError(f"preshuffle_e8m0 needs a 2-D uint8 tensor, got {scales.dtype} {tuple(scales.shape)}")
+    R, G = scales.shape
+    chunks = -(-G // PS_CHUNK_GROUPS)
+    padded = torch.full((R, chunks * PS_CHUNK_GROUPS), 127, dtype=torch.uint8, device=scales.device)
+    padded[:, :G] = scales
+    grouped = padded.reshape(R, chunks, PS_CHUNK_GROUPS)[:, :, _ps_group_order(scales.device)]
+    return grouped.permute(1, 0, 2).contiguous()
+
+
+def unshuffle_e8m0(ps: torch.Tensor, groups: int) -> torch.Tensor:
+    """Inverse of preshuffle_e8m0: (chunks, R, 32) -> (R, groups)."""
+    chunks, R, w = ps.shape
+    if w != PS_CHUNK_GROUPS or groups > chunks * PS_CHUNK_GROUPS:
+        raise ValueError(f"not a preshuffled scale tensor for {groups} groups: {tuple(ps.shape)}")
+    out = torch.empty(R, chunks, PS_CHUNK_GROUPS, dtype=ps.dtype, device=ps.device)
+    out[:, :, _ps_group_order(ps.device)] = ps.permute(1, 0, 2)
+    return out.reshape(R, chunks * PS_CHUNK_GROUPS)[:, :groups].contiguous()

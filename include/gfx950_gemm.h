@@ -46,8 +46,9 @@ enum {
   G9_ERR_SCRATCH = 7    /* g9_gemm_a16w16_noalloc: the call needs more than its static scratch buffer */
 };
 
-/* Element / output types. */
-enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3 };
+/* Element / output types.  G9_FP4P is MXFP4 with preshuffled scales (the
+ * operand type of g9_gemm_a4w4_preshuffled, for g9_kernel_name). */
+enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3, G9_FP4P = 4 };
 
 /* Tile schedules.  G9_SCHED_SPLITK has no counterpart in the reference: it is
  * for callers whose grids leave most CUs idle (few-row GEMMs, one GPU's
@@ -118,6 +119,28 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
                  int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
                  int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/*
+ * a4w4 with preshuffled E8M0 scales: the operands, output and results of
+ * g9_gemm_a4w4 (bit-identical for the same scale values), with each operand's
+ * scales in the kernel's read order instead of row-major.  Scales of stages
+ * 4c..4c+3 (K values 1024c..1024c+1023) form chunk c, and row r of chunk c is
+ * the 32 bytes at scales + c * stride_asc + 32 * r, whose byte 8g + 2s + h holds
+ * the E8M0 scale of K group 32c + 8s + 4h + g (g, s in 0..3, h in 0..1);
+ * chunks past K/32 groups may hold anything.  quant.preshuffle_e8m0 builds this
+ * layout (stride = 32 * rows); the scales are 16-byte aligned, stride_asc and
+ * stride_bsc multiples of 16 of at least 32 * M and 32 * N bytes (ignored when
+ * K <= 1024: one chunk).  Each lane
+ * then reads its scales of four stages with one LDS read and the scale DMAs
+ * move contiguous KiB.  Data-parallel schedule, 4 waves.  No counterpart in the
+ * reference: its roadmap lists preshuffled scales (its ROADMAP.md,
+ * "4-bit + Scales", "Document preshuffling").
+ */
+int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                             int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                             int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                             int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Grouped ("MoE") GEMMs over E experts, 4-wave, data-parallel tiles.  The

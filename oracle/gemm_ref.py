@@ -182,6 +182,24 @@ def quant_mxfp4(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 # ---------------------------------------------------------------------------
 
 
+def preshuffle_e8m0(scales: np.ndarray) -> np.ndarray:
+    """Restates, with explicit loops over the index definition, the preshuffled
+    MXFP4 scale layout of g9_gemm_a4w4_preshuffled (no counterpart in the
+    reference, whose ROADMAP.md lists preshuffled scales as planned): out[c, r,
+    8g + 2s + h] = scales[r, 32c + 8s + 4h + g]; groups past the end read 127."""
+    R, G = scales.shape
+    chunks = -(-G // 32)
+    out = np.full((chunks, R, 32), 127, dtype=np.uint8)
+    for c in range(chunks):
+        for g in range(4):
+            for s in range(4):
+                for h in range(2):
+                    grp = 32 * c + 8 * s + 4 * h + g
+                    if grp < G:
+                        out[c, :, 8 * g + 2 * s + h] = scales[:, grp]
+    return out
+
+
 def gemm_f32(a: np.ndarray, b_nk: np.ndarray) -> np.ndarray:
     """C = A . B^T in fp32 (numpy/BLAS), A (M, K), B (N, K)."""
     return np.asarray(a, dtype=np.float32) @ np.asarray(b_nk, dtype=np.float32).T
