@@ -276,42 +276,81 @@ def time_serialized(launch, n=1000, last=100):
     return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / last
 
 
-def cpu_baseline(dtype: str, M: int, N: int, K: int, seed: int):
-    """The oracle's fp32 GEMM of the dequantized operands on this host, on a
-    row sample sized to a few seconds; TFLOPS scaled per FLOP."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _dequantized_operands(dtype: str, M: int, N: int, K: int, seed: int, dev):
+    """The BASELINE configuration's operands of `dtype`, drawn as make_case
+    draws them (CPU generator, quantized on the GPU), dequantized to fp32 on
+    the host with the oracle's formulas (not timed)."""
     import numpy as np
+    import torch
+
+    from gfx950_gluon_tutorials_amd import quant
+    from oracle import gemm_ref as R
+
+    gen = torch.Generator().manual_seed(seed)
+    if dtype == "fp16":
+        a = (torch.randn(M, K, generator=gen) * 0.1).half().float().numpy()
+        b = (torch.randn(N, K, generator=gen) * 0.1).half().float().numpy()
+        return a, b
+    if dtype == "bf8":
+        qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=gen).to(dev))
+        qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=gen).to(dev))
+        a = R.e5m2_to_f32(qa.view(torch.uint8).cpu().numpy()) * np.float32(sa.item())
+        b = R.e5m2_to_f32(qb.view(torch.uint8).cpu().numpy()) * np.float32(sb.item())
+        return a, b
+    pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=gen).to(dev))
+    pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=gen).to(dev))
+    return (R.mxfp4_dequant(pa.cpu().numpy(), sa.cpu().numpy()),
+            R.mxfp4_dequant(pb.cpu().numpy(), sb.cpu().numpy()))
+
+
+def cpu_baseline(M: int, N: int, K: int, dev, seeds: dict) -> dict:
+    """The reference's CPU path (torch.matmul in fp32 on the dequantized
+    operands, oracle.gemm_ref.torch_matmul_f32) on this host, for the fp16,
+    bf8 and mxfp4 configurations at their full size: 1 warm-up, then the
+    median of 3; dequantization is outside the timing.  The headline fields
+    are fp16's; per_dtype holds all three."""
+    import torch
 
     from oracle import gemm_ref as R
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
-    except Exception:  # threadpoolctl missing: report the visible cores
-        threads = os.cpu_count() or 1
-    rng = np.random.default_rng(seed)
-    rows = 512
-    a = rng.standard_normal((rows, K), dtype=np.float32) * 0.1
-    b = rng.standard_normal((N, K), dtype=np.float32) * 0.1
-    if dtype == "fp16":
-        a = a.astype(np.float16).astype(np.float32)
-        b = b.astype(np.float16).astype(np.float32)
-    R.gemm_f32(a[:64], b)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        R.gemm_f32(a, b)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    tflops = 2.0 * rows * N * K / t / 1e12
+    per = {}
+    for dt in ("fp16", "bf8", "mxfp4"):
+        a, b = _dequantized_operands(dt, M, N, K, seeds[dt], dev)
+        R.torch_matmul_f32(a, b)  # warm-up
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            R.torch_matmul_f32(a, b)
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[1]
+        per[dt] = {"tflops": round(2.0 * M * N * K / t / 1e12, 4), "seconds": round(t, 4),
+                   "sample": f"full {M}x{N}x{K}, seed {seeds[dt]}"}
+        print(f"# cpu baseline {dt}: {per[dt]['tflops']:.3f} TFLOPS ({t:.3f} s, torch.matmul fp32, "
+              f"{torch.get_num_threads()} threads)", flush=True)
+        del a, b
     return {
-        "value": round(tflops, 4),
+        "value": per["fp16"]["tflops"],
         "unit": "TFLOPS",
-        "cores": int(threads),
+        "cores": int(torch.get_num_threads()),
         "kind": "port",
-        "sample": f"fp32 GEMM of dequantized operands, {rows}x{N}x{K} rows of the {M}x{N}x{K} workload, "
-                  f"median of 3 (oracle.gemm_ref.gemm_f32, numpy BLAS)",
-        "host_cpus": os.cpu_count(),
+        "sample": f"torch.matmul fp32 of the dequantized operands at the full {M}x{N}x{K} size of each BASELINE "
+                  f"configuration (fp16 seed 1, bf8 seed 2, mxfp4 seed 3), 1 warm-up then median of 3, "
+                  f"dequantization untimed (oracle.gemm_ref.torch_matmul_f32); value = fp16",
+        "per_dtype": per,
+        "torch_threads": int(torch.get_num_threads()),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model(),
     }
 
 
@@ -486,7 +525,9 @@ def ksweep(args, dev) -> dict:
 def make_vendor_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int):
     """launch(i) running ROCm's library GEMM (hipBLASLt through torch) on the
     same kind of operands as make_case: torch.matmul for fp16/bf16,
-    torch._scaled_mm (e5m2 x e5m2 -> bf16, per-tensor scales) for bf8."""
+    torch._scaled_mm (e5m2 x e5m2 -> bf16, per-tensor scales) for bf8, and
+    torch._scaled_mm on float4_e2m1fn_x2 operands with float8_e8m0fnu per-32
+    scales (-> bf16) for mxfp4."""
     import torch
 
     from gfx950_gluon_tutorials_amd import quant
@@ -499,10 +540,15 @@ def make_vendor_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: 
             a = (torch.randn(M, K, generator=gen) * 0.1).to(tdt).to(dev)
             b = (torch.randn(N, K, generator=gen) * 0.1).to(tdt).to(dev)
             sets.append((a, b, torch.empty(M, N, dtype=tdt, device=dev)))
-        else:
+        elif dtype == "bf8":
             qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=gen).to(dev))
             qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=gen).to(dev))
             sets.append((qa, qb, sa.reshape(()).float(), sb.reshape(()).float()))
+        else:
+            pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=gen).to(dev))
+            pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=gen).to(dev))
+            sets.append((pa.view(torch.float4_e2m1fn_x2), pb.view(torch.float4_e2m1fn_x2),
+                         sa.view(torch.float8_e8m0fnu).flatten(), sb.view(torch.float8_e8m0fnu).flatten()))
 
     def launch(i, schedule="dp"):
         x = sets[i % nsets]
@@ -602,9 +648,9 @@ def main():
                 print(f"#   steady state {tel['launch_us']:.1f} us ({tel['tflops']:.0f} TFLOPS) at "
                       f"{tel['power_w']:.0f} W, GFX clock {tel['gfx_clock_mhz']} MHz (amd-smi, {tel['samples']} samples)",
                       flush=True)
-        if args.vendor and not args.only and kk == K and w == 4 and dt in ("fp16", "bf16", "bf8"):
+        if args.vendor and not args.only and kk == K and w == 4 and dt in ("fp16", "bf16", "bf8", "mxfp4", "mxfp4ps"):
             try:
-                vlaunch = make_vendor_case(dt, M, N, kk, seeds[dt], dev, nsets)
+                vlaunch = make_vendor_case("mxfp4" if dt == "mxfp4ps" else dt, M, N, kk, seeds[dt], dev, nsets)
             except Exception as e:  # no library kernel for this type on this build
                 results[key]["vendor"] = {"library": "hipBLASLt via torch", "error": str(e).splitlines()[0][:120]}
             else:
@@ -615,7 +661,7 @@ def main():
                     t_lib.append(time_case(vlaunch, max(20, args.steps // 2), 20, settle_s=0.3))
                 mo, ml = sorted(t_ours)[1], sorted(t_lib)[1]
                 tf_o, tf_l = 2.0 * M * N * kk / (mo * 1e-3) / 1e12, 2.0 * M * N * kk / (ml * 1e-3) / 1e12
-                results[key]["vendor"] = {"library": "hipBLASLt via torch." + ("matmul" if dt != "bf8" else "_scaled_mm"),
+                results[key]["vendor"] = {"library": "hipBLASLt via torch." + ("matmul" if dt in ("fp16", "bf16") else "_scaled_mm"),
                                           "tflops": round(tf_l, 2), "ours_interleaved_tflops": round(tf_o, 2),
                                           "ours_over_library": round(tf_o / tf_l, 4)}
                 print(f"#   same box, interleaved: ours {tf_o:.1f} vs hipBLASLt {tf_l:.1f} TFLOPS ({tf_o / tf_l:.3f}x)",
@@ -718,7 +764,7 @@ def main():
         "moe": moe,
     }
     if args.cpu_baseline and not args.only:
-        line["cpu_baseline"] = cpu_baseline(head.split("_")[0], M, N, K, seeds[head.split("_")[0]])
+        line["cpu_baseline"] = cpu_baseline(M, N, K, dev, seeds)
     print(json.dumps(line), flush=True)
 
 

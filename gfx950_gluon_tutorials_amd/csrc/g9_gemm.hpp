@@ -153,7 +153,7 @@ struct GemmParams {
 constexpr int kTile = 256;
 constexpr int kRowBytes = 128;              // bytes of one operand row per stage
 constexpr int kSubBytes = 128 * kRowBytes;  // one sub-buffer (16 KiB)
-constexpr int kStageRow = 528;              // epilogue staging row pitch (bytes)
+constexpr int kStageRow = 528;              // epilogue staging row pitch (bytes; see store_tile)
 // FP4 E8M0 scales are staged in chunks of kScChunk stages: one chunk holds
 // kScChunk * 8 bytes of each of the tile's 256 A rows and 256 B rows (chunk
 // rows 0-255 = A, 256-511 = B), and two chunk slots sit after the operand
@@ -290,7 +290,16 @@ struct Shape {
     for (int q = 1; q <= 6; ++q) n += dmas(((pos - q) % kRegions + kRegions) % kRegions);
     return n;
   }
-  static_assert(vm_wait(0) < 64, "vmcnt is 6 bits");
+  // Ping-pong (8-wave): at the end of region pos's memory cluster, the DMAs
+  // issued 6 regions earlier must have landed (the next memory cluster reads
+  // them, and the other wave group reads them one cluster later still):
+  // vmcnt(DMAs of region pos and the 5 before it).
+  static constexpr int vm_wait_pp(int pos) {
+    int n = 0;
+    for (int q = 0; q <= 5; ++q) n += dmas(((pos - q) % kRegions + kRegions) % kRegions);
+    return n;
+  }
+  static_assert(vm_wait(0) < 64 && vm_wait_pp(0) < 64, "vmcnt is 6 bits");
 };
 
 template <class G>
@@ -556,17 +565,20 @@ struct Pipe {
     }
     if constexpr (I::kPreshuffled) {
       // Preshuffled scales (quant.preshuffle_e8m0): chunk c (stages 4c..4c+3)
-      // of row r is 32 bytes at c * cstride + r * 32, byte 8g + 2st + h being
-      // the scale of group 8st + 4h + g (lane group g, stage st of the chunk,
-      // MFMA step h).  A chunk part of 32 rows is one contiguous KiB, so every
+      // of row r is 32 bytes at c * cstride + r * 32, byte 8j + 2st + h being
+      // the scale of group 8st + 4h + g (lane group g = j ^ ((r >> 2) & 3),
+      // stage st of the chunk, MFMA step h).  A chunk part of 32 rows is one contiguous KiB, so every
       // part DMA shares one offset and moves by 1024 bytes through its
       // immediate, in global memory and LDS alike.  The resource covers the
       // operand's whole scale array; rows past the end in the last chunk read
       // zero, rows past the end in earlier chunks read the next chunk's rows
       // (they only meet A or B rows that read zero and outputs that are not
       // stored).  The LDS chunk slot holds the tile's 512 rows of 32 bytes in
-      // the same order, and lane (row, g) reads its 8 bytes at row * 32 + 8g:
-      // a fragment's 16 rows are 512 contiguous bytes, free of bank conflicts.
+      // the same order, and lane (row, g) reads its 8 bytes at row * 32 +
+      // 8 * (g ^ ((row >> 2) & 3)): the XOR puts the 16 rows of a read pass
+      // on distinct bank pairs (without it rows r and r + 4 share one: 2-way
+      // conflicts, measured).  Fragment rows start at multiples of 16, so the
+      // XOR depends on the lane's row rr only.
       const int xw = wave / (G::NW / 4);
       const int r0 = (wave % (G::NW / 4)) * G::kScRows;
       const bool sa = xw < 2;
@@ -577,8 +589,9 @@ struct Pipe {
       const int hrow = (sa ? tm : tn) * kTile + (xw & 1) * 128;
       vS[0] = (u32)(hrow + r0) * kScRowBytes + 16u * lane;
       msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
-      bS[0][0] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + 8 * gi);
-      bS[1][0] = opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 8 * gi);
+      const u32 unit = 8u * (u32)(gi ^ ((rr >> 2) & 3));
+      bS[0][0] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + unit);
+      bS[1][0] = opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + unit);
       sel = 0;
     } else if constexpr (I::kScaled) {
       // The wave loads chunk rows [xw * 128 + r0, + kScRows) of the 512: half
@@ -770,6 +783,29 @@ G9_DEV void settle_acc(Acc<G>& acc) {
 // A fragment, B fragment), then whatever the slot table puts after it, then a
 // hard scheduling fence (the MFMAs are inline assembly, which the scheduler's
 // instruction-class masks do not cover, so only a full fence pins the order).
+// MFMA number K of the region at body position POS (step-major: step, A
+// fragment, B fragment).  Snake order over the fragment grid: odd A fragments
+// walk the B fragments backwards, so consecutive MFMAs share one operand
+// register set.  The chip is power-limited in this loop and fewer operand
+// changes cost less energy (measured: about 0.8% less time for every dtype,
+// identical results).
+template <Op OP, class G, int POS, int K>
+G9_DEV void region_mfma(QAcc<G>& acc, const ScRegs<OP, G>& sr, const FragSet<G>& bx, const FragSet<G>& ay) {
+  constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j0 = K % G::FN;
+  constexpr int j = (i % 2) ? G::FN - 1 - j0 : j0;
+  if constexpr (OpInfo<OP>::kPreshuffled) {
+    // Region POS % 4 is quadrant (A0,B0), (A0,B1), (A1,B1), (A1,B0); its
+    // stage is stage POS / 4 % 4 of chunk POS / 16 of the body.
+    constexpr int quad = POS % 4, st = (POS / 4) % kScChunk, cp = (POS / 16) % 2;
+    const u32x2& sa = sr.a[quad >= 2 ? 1 : 0][i];
+    const u32x2& sb = (quad == 1 || quad == 2) ? sr.b1[j] : sr.b0[cp][j];
+    mfma_scaled<2 * (st & 1) + e>(acc[i][j], bx[j].c[e], ay[i].c[e], (st >> 1) ? sb.y : sb.x,
+                                  (st >> 1) ? sa.y : sa.x);
+  } else {
+    mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
+  }
+}
+
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS, int K>
 G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u32 mb, u32 ms, QAcc<G>& acc,
                         ScRegs<OP, G>& sr, const FragSet<G>& bx, const FragSet<G>& ay, FragSet<G>& nxt) {
@@ -786,23 +822,7 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
   // the other parts to the next chunk's slot.
   constexpr int part = Sh::sc_part(POS);
   constexpr int kDSSlot = part == 0 ? (POS / 16) % 2 : (POS / 16 + 1) % 2;
-  // Snake order over the fragment grid: odd A fragments walk the B fragments
-  // backwards, so consecutive MFMAs share one operand register set.  The chip
-  // is power-limited in this loop and fewer operand changes cost less energy
-  // (measured: about 0.8% less time for every dtype, identical results).
-  constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j0 = K % G::FN;
-  constexpr int j = (i % 2) ? G::FN - 1 - j0 : j0;
-  if constexpr (OpInfo<OP>::kPreshuffled) {
-    // Region POS % 4 is quadrant (A0,B0), (A0,B1), (A1,B1), (A1,B0); its
-    // stage is stage POS / 4 % 4 of chunk POS / 16 of the body.
-    constexpr int quad = POS % 4, st = (POS / 4) % kScChunk, cp = (POS / 16) % 2;
-    const u32x2& sa = sr.a[quad >= 2 ? 1 : 0][i];
-    const u32x2& sb = (quad == 1 || quad == 2) ? sr.b1[j] : sr.b0[cp][j];
-    mfma_scaled<2 * (st & 1) + e>(acc[i][j], bx[j].c[e], ay[i].c[e], (st >> 1) ? sb.y : sb.x,
-                                  (st >> 1) ? sa.y : sa.x);
-  } else {
-    mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
-  }
+  region_mfma<OP, G, POS, K>(acc, sr, bx, ay);
   constexpr int q = K - S::kPre;
   if constexpr (q >= 0) {
     static_for<S::NR>([&](auto R) {
@@ -876,6 +896,74 @@ G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP,
   }(std::make_integer_sequence<int, S::NM - S::kPre>{});
 }
 
+// ---------------------------------------------------------------------------
+// 8-wave ping-pong.  The two waves of a SIMD (waves w and w + 4) run the same
+// region sequence one cluster apart: each region is split into an MFMA
+// cluster (its MFMAs only, at wave priority 0) and a memory cluster (the next
+// region's LDS reads and this region's DMAs, at priority 1), with a workgroup
+// barrier at every cluster boundary.  Waves 4-7 take one extra barrier before
+// the loop, so whenever waves 0-3 run an MFMA cluster waves 4-7 run a memory
+// cluster and the other way round: one wave of each SIMD keeps the matrix
+// unit busy while the other issues its reads and DMAs beside it, and the
+// memory cluster's higher priority lets it issue in the MFMA stream's free
+// slots.  Waves 0-3 take the matching extra barrier after the loop.
+//
+// Ordering, with groups a cluster apart:
+//  * a memory cluster ends with lgkmcnt(0) before its barrier, so its reads
+//    have landed before any wave passes the barrier -- the next MFMA cluster's
+//    operands, and the sub-buffer they came from is free for the DMA the next
+//    memory cluster issues (the other group's reads of it ended one barrier
+//    earlier);
+//  * a memory cluster also waits, before its barrier, for its DMAs of 6
+//    regions earlier: the next memory cluster of the leading group reads them
+//    after that barrier.  The lagging group waits one region earlier than its
+//    own reads need, so the DMA lead is 6 regions instead of 7.
+// ---------------------------------------------------------------------------
+#ifndef G9_PINGPONG
+#define G9_PINGPONG 1
+#endif
+template <class G>
+constexpr bool kPingPong = G9_PINGPONG != 0 && G::NW == 8;
+
+template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS>
+G9_DEV void region_pp(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP, G>& sr, const FragSet<G>& bx,
+                      const FragSet<G>& ay, FragSet<G>& nxt) {
+  constexpr int NF = RX < 2 ? G::FM : G::FN;
+  using Sh = Shape<OP, G>;
+  static_assert(!OpInfo<OP>::kPreshuffled, "preshuffled scales run 4-wave");
+  constexpr int ks = POS / 4 + (POS % 4 >= 2 ? 1 : 0);
+  constexpr int kSSlot = (ks / kScChunk) % 2, kSt = ks % kScChunk;
+  constexpr int part = Sh::sc_part(POS);
+  constexpr int kDSSlot = part == 0 ? (POS / 16) % 2 : (POS / 16 + 1) % 2;
+  // MFMA cluster.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(0);
+  static_for<Sh::NM>([&](auto K) {
+    region_mfma<OP, G, POS, decltype(K)::value>(acc, sr, bx, ay);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  barrier();
+  // Memory cluster.
+  __builtin_amdgcn_s_setprio(1);
+  const rsrc_t r = P.src(DX);
+  const u32 soff = P.stage_off(ds);
+  const u32 mb = opaque_s(P.mrow);
+  static_for<G::NC * NF>([&](auto R) { P.template read_chunk<RX, RSLOT, decltype(R)::value>(nxt); });
+  if constexpr (OpInfo<OP>::kScaled)
+    static_for<NF>([&](auto F) { P.template read_scales<RX, kSSlot, kSt, decltype(F)::value>(nxt); });
+  static_for<Sh::D>([&](auto J) { P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb); });
+  if constexpr (part >= 0) {
+    const u32 soff_sc = P.chunk_off(s + kScChunk * (POS / 16) + (part == 0 ? 2 : 1) * kScChunk);
+    P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, opaque_s(P.msc));
+  }
+  if constexpr (OpInfo<OP>::kScaled && G::MD == 16) {
+    waitcnt<63, 0>();
+    P.template gather_scales<RX>(nxt);
+  }
+  waitcnt<Sh::vm_wait_pp(POS), 0>();
+  barrier();
+}
+
 // Stage K of the body starting at stage s.  Even stages (operand slot 0): B0
 // fragments in x; B1 fragments go to y, and after they are consumed the next
 // stage's B0 fragments go to y as well.  Odd stages (slot 1): B0 in y; B1 to
@@ -884,16 +972,23 @@ template <Op OP, class G, int K>
 G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, ScRegs<OP, G>& sr, FragSet<G>& at, FragSet<G>& ab,
                   FragSet<G>& x, FragSet<G>& y) {
   constexpr int POS = 4 * K;
+  auto rg = [&]<int RX, int RSLOT, int DX, int DSLOT, int P_>(int ds, QAcc<G>& a, const FragSet<G>& bx,
+                                                                const FragSet<G>& ay, FragSet<G>& nxt) {
+    if constexpr (kPingPong<G>)
+      region_pp<OP, G, RX, RSLOT, DX, DSLOT, P_>(P, s, ds, a, sr, bx, ay, nxt);
+    else
+      region<OP, G, RX, RSLOT, DX, DSLOT, P_>(P, s, ds, a, sr, bx, ay, nxt);
+  };
   if constexpr (K % 2 == 0) {
-    region<OP, G, 3, 0, 2, 0, POS + 0>(P, s, s + K + 2, acc[0][0], sr, x, at, y);
-    region<OP, G, 1, 0, 3, 0, POS + 1>(P, s, s + K + 2, acc[0][1], sr, y, at, ab);
-    region<OP, G, 0, 1, 1, 0, POS + 2>(P, s, s + K + 2, acc[1][1], sr, y, ab, at);
-    region<OP, G, 2, 1, 0, 1, POS + 3>(P, s, s + K + 3, acc[1][0], sr, x, ab, y);
+    rg.template operator()<3, 0, 2, 0, POS + 0>(s + K + 2, acc[0][0], x, at, y);
+    rg.template operator()<1, 0, 3, 0, POS + 1>(s + K + 2, acc[0][1], y, at, ab);
+    rg.template operator()<0, 1, 1, 0, POS + 2>(s + K + 2, acc[1][1], y, ab, at);
+    rg.template operator()<2, 1, 0, 1, POS + 3>(s + K + 3, acc[1][0], x, ab, y);
   } else {
-    region<OP, G, 3, 1, 2, 1, POS + 0>(P, s, s + K + 2, acc[0][0], sr, y, at, x);
-    region<OP, G, 1, 1, 3, 1, POS + 1>(P, s, s + K + 2, acc[0][1], sr, x, at, ab);
-    region<OP, G, 0, 0, 1, 1, POS + 2>(P, s, s + K + 2, acc[1][1], sr, x, ab, at);
-    region<OP, G, 2, 0, 0, 0, POS + 3>(P, s, s + K + 3, acc[1][0], sr, y, ab, x);
+    rg.template operator()<3, 1, 2, 1, POS + 0>(s + K + 2, acc[0][0], y, at, x);
+    rg.template operator()<1, 1, 3, 1, POS + 1>(s + K + 2, acc[0][1], x, at, ab);
+    rg.template operator()<0, 0, 1, 1, POS + 2>(s + K + 2, acc[1][1], x, ab, at);
+    rg.template operator()<2, 0, 0, 0, POS + 3>(s + K + 3, acc[1][0], y, ab, x);
   }
 }
 
@@ -933,8 +1028,9 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   P.template issue<1, 1>(s0 + 1);
   if constexpr (kScaled) P.template issue_chunk<1, 0>(s0 + kScChunk);
   // A0(s0) and B0(s0) landed (and chunk 0, issued before them): read them,
-  // then (once every wave has) refill A0 slot 0 with stage s0+2.
-  constexpr int kFirst = 6 * Sh::D + (kScaled ? 1 : 0);
+  // then (once every wave has) refill A0 slot 0 with stage s0+2.  Ping-pong:
+  // B1(s0) as well, which the first memory cluster reads.
+  constexpr int kFirst = (kPingPong<G> ? 5 : 6) * Sh::D + (kScaled ? 1 : 0);
   waitcnt<kFirst, 0>();
   barrier();
   FragSet<G> at, ab, x, y;
@@ -954,6 +1050,9 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   }
   barrier();
   P.template issue<0, 0>(s0 + 2);
+  // Ping-pong: waves 4-7 start one cluster behind.
+  const bool lag = kPingPong<G> && P.wave >= 4;
+  if (lag) barrier();
   // The accumulators were just written by VALU (zeroing or a partial tile):
   // wait states before the first MFMA reads them.
   mfma_drain();
@@ -967,6 +1066,11 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   if (s < s1) {
     tail<OP, G, 0>(P, s, s1 - s, acc, sr, at, ab, x, y);
     settle_acc<G>(acc);
+  }
+  if constexpr (kPingPong<G>) {
+    // Waves 0-3 match the lagging group's last barrier; back to priority 0.
+    if (!lag) barrier();
+    __builtin_amdgcn_s_setprio(0);
   }
   waitcnt<0, 0>();
   barrier();
@@ -985,6 +1089,17 @@ G9_DEV void zero_acc(Acc<G>& acc) {
 // Converts the tile to 16-bit (after multiplying by `scale`), stages it in LDS
 // and writes it to C with coalesced 16-byte row chunks, masking rows >= M and
 // columns >= N.  LDS must be free on entry; it is free again on return.
+//
+// Staging layout: row m of the tile at m * 528 bytes, rows 16-byte aligned so
+// the 16-byte reads stay aligned.  Measured on gfx950 (SQ_LDS_BANK_CONFLICT of
+// probe kernels), a 64-lane ds_write_b64 is served 16 consecutive lanes at a
+// time over 32 banks, so a write pass (16 rows of one 8-byte unit) sees the
+// rows' 4-bank offsets wrap after 8 rows: 4 conflict cycles per write, 1024
+// per workgroup.  A conflict-free variant (8-byte units XOR-swizzled by row,
+// read back as swapped 16-byte pairs) measured 0 conflicts but 0.5-1.0% more
+// time for every type, interleaved in one process: the epilogue is bound by
+// the C write to HBM, and its extra address and swap instructions lengthened
+// it by ~1.5k cycles.
 template <int OUT, class G>
 G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& acc, float scale) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

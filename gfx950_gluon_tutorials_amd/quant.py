@@ -15,8 +15,8 @@ the BF8 and MXFP4 benchmark configurations:
   packed two per byte with the even k in the low nibble.
 * ``preshuffle_e8m0(scales)``: the MXFP4 scales in the read order of the
   preshuffled-scale kernel (``g9_gemm_a4w4_preshuffled``): chunk-major, 32
-  bytes per row per chunk of 32 K groups (1024 K values), byte 8g + 2s + h of a
-  chunk row holding group 8s + 4h + g.
+  bytes per row per chunk of 32 K groups (1024 K values), byte 8j + 2s + h of
+  chunk row r holding group 8s + 4h + g with g = j ^ ((r >> 2) & 3).
 """
 
 from __future__ import annotations
@@ -83,11 +83,14 @@ def dequantize_mxfp4(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor
 PS_CHUNK_GROUPS = 32
 
 
-def _ps_group_order(device=None) -> torch.Tensor:
-    """Position j of a preshuffled chunk row holds group order[j] of the chunk:
-    j = 8g + 2s + h  <->  group 8s + 4h + g."""
-    j = torch.arange(PS_CHUNK_GROUPS, device=device)
-    g, s, h = j // 8, (j % 8) // 2, j % 2
+def _ps_group_order(rows: int, device=None) -> torch.Tensor:
+    """(rows, 32): position 8j + 2s + h of preshuffled chunk row r holds group
+    8s + 4h + g of the chunk, g = j ^ ((r >> 2) & 3).  The row-dependent XOR
+    puts the 16 rows one LDS read serves on distinct bank pairs."""
+    p = torch.arange(PS_CHUNK_GROUPS, device=device)
+    j, s, h = p // 8, (p % 8) // 2, p % 2
+    r = torch.arange(rows, device=device).unsqueeze(1)
+    g = j ^ ((r >> 2) & 3)
     return 8 * s + 4 * h + g
 
 
@@ -102,8 +105,9 @@ def preshuffle_e8m0(scales: torch.Tensor) -> torch.Tensor:
     chunks = -(-G // PS_CHUNK_GROUPS)
     padded = torch.full((R, chunks * PS_CHUNK_GROUPS), 127, dtype=torch.uint8, device=scales.device)
     padded[:, :G] = scales
-    grouped = padded.reshape(R, chunks, PS_CHUNK_GROUPS)[:, :, _ps_group_order(scales.device)]
-    return grouped.permute(1, 0, 2).contiguous()
+    grouped = padded.reshape(R, chunks, PS_CHUNK_GROUPS)
+    order = _ps_group_order(R, scales.device).unsqueeze(1).expand(R, chunks, PS_CHUNK_GROUPS)
+    return torch.gather(grouped, 2, order).permute(1, 0, 2).contiguous()
 
 
 def unshuffle_e8m0(ps: torch.Tensor, groups: int) -> torch.Tensor:
@@ -112,5 +116,6 @@ def unshuffle_e8m0(ps: torch.Tensor, groups: int) -> torch.Tensor:
     if w != PS_CHUNK_GROUPS or groups > chunks * PS_CHUNK_GROUPS:
         raise ValueError(f"not a preshuffled scale tensor for {groups} groups: {tuple(ps.shape)}")
     out = torch.empty(R, chunks, PS_CHUNK_GROUPS, dtype=ps.dtype, device=ps.device)
-    out[:, :, _ps_group_order(ps.device)] = ps.permute(1, 0, 2)
+    order = _ps_group_order(R, ps.device).unsqueeze(1).expand(R, chunks, PS_CHUNK_GROUPS)
+    out.scatter_(2, order, ps.permute(1, 0, 2))
     return out.reshape(R, chunks * PS_CHUNK_GROUPS)[:, :groups].contiguous()

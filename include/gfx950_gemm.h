@@ -125,9 +125,9 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
  * g9_gemm_a4w4 (bit-identical for the same scale values), with each operand's
  * scales in the kernel's read order instead of row-major.  Scales of stages
  * 4c..4c+3 (K values 1024c..1024c+1023) form chunk c, and row r of chunk c is
- * the 32 bytes at scales + c * stride_asc + 32 * r, whose byte 8g + 2s + h holds
- * the E8M0 scale of K group 32c + 8s + 4h + g (g, s in 0..3, h in 0..1);
- * chunks past K/32 groups may hold anything.  quant.preshuffle_e8m0 builds this
+ * the 32 bytes at scales + c * stride_asc + 32 * r, whose byte 8j + 2s + h holds
+ * the E8M0 scale of K group 32c + 8s + 4h + g with g = j ^ ((r >> 2) & 3)
+ * (j, s in 0..3, h in 0..1); groups past K/32 may hold anything.  quant.preshuffle_e8m0 builds this
  * layout (stride = 32 * rows); the scales are 16-byte aligned, stride_asc and
  * stride_bsc multiples of 16 of at least 32 * M and 32 * N bytes (ignored when
  * K <= 1024: one chunk).  Each lane

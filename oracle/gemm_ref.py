@@ -186,18 +186,34 @@ def preshuffle_e8m0(scales: np.ndarray) -> np.ndarray:
     """Restates, with explicit loops over the index definition, the preshuffled
     MXFP4 scale layout of g9_gemm_a4w4_preshuffled (no counterpart in the
     reference, whose ROADMAP.md lists preshuffled scales as planned): out[c, r,
-    8g + 2s + h] = scales[r, 32c + 8s + 4h + g]; groups past the end read 127."""
+    8j + 2s + h] = scales[r, 32c + 8s + 4h + g] with g = j ^ ((r >> 2) & 3);
+    groups past the end read 127."""
     R, G = scales.shape
     chunks = -(-G // 32)
     out = np.full((chunks, R, 32), 127, dtype=np.uint8)
-    for c in range(chunks):
-        for g in range(4):
-            for s in range(4):
-                for h in range(2):
-                    grp = 32 * c + 8 * s + 4 * h + g
-                    if grp < G:
-                        out[c, :, 8 * g + 2 * s + h] = scales[:, grp]
+    for r in range(R):
+        for c in range(chunks):
+            for j in range(4):
+                g = j ^ ((r >> 2) & 3)
+                for s in range(4):
+                    for h in range(2):
+                        grp = 32 * c + 8 * s + 4 * h + g
+                        if grp < G:
+                            out[c, r, 8 * j + 2 * s + h] = scales[r, grp]
     return out
+
+
+def torch_matmul_f32(a: np.ndarray, b_nk: np.ndarray):
+    """The reference's CPU correctness path as BASELINE names it: torch.matmul
+    in fp32 of the (dequantized) operands, C = A . B_nk^T
+    (kernels/gemm/intra_wave/a4w4/bench.py:149-164 torch_reference; the fp16
+    and bf8 benches' torch.matmul, a16w16/bench.py:167-187, a8w8/bench.py:129-142,
+    run here in fp32 on the CPU).  Returns a torch fp32 tensor."""
+    import torch
+
+    at = torch.as_tensor(np.ascontiguousarray(a, dtype=np.float32))
+    bt = torch.as_tensor(np.ascontiguousarray(b_nk, dtype=np.float32))
+    return torch.matmul(at, bt.T)
 
 
 def gemm_f32(a: np.ndarray, b_nk: np.ndarray) -> np.ndarray:

@@ -266,3 +266,18 @@ def test_moe_ref_passes_row_and_expert_operands():
     c = R.moe_ref(R.a4w4_ref_f32, a, b, [0, 1, 1, 4], a_sc, expert_args=(b_sc,))
     np.testing.assert_array_equal(c[0], [K, K])
     np.testing.assert_array_equal(c[1:], np.full((3, N), K * 4.0))
+
+
+def test_torch_matmul_f32_against_brute_force():
+    """The CPU baseline's restatement of the reference's torch.matmul path:
+    exact on small integers (every partial sum is exact in fp32) and within
+    fp32 rounding of a float64 triple loop on random values."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(-8, 9, (7, 33)).astype(np.float32)
+    b = rng.integers(-8, 9, (5, 33)).astype(np.float32)
+    want = [[sum(int(a[i, k]) * int(b[j, k]) for k in range(33)) for j in range(5)] for i in range(7)]
+    np.testing.assert_array_equal(R.torch_matmul_f32(a, b).numpy(), np.array(want, dtype=np.float32))
+    x = rng.standard_normal((6, 40)).astype(np.float32)
+    y = rng.standard_normal((3, 40)).astype(np.float32)
+    ref = np.array([[sum(float(x[i, k]) * float(y[j, k]) for k in range(40)) for j in range(3)] for i in range(6)])
+    np.testing.assert_allclose(R.torch_matmul_f32(x, y).numpy(), ref, rtol=1e-5, atol=1e-5)
