@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in ``include/gfx950_gemm.h``.
+"""ctypes binding of the C ABI in ``include/gfx950_gemm.h`` and
+``include/gfx950_fmha.h``.
 
 The library is loaded from this package directory (built by ``build.py``).
 There is no fallback: if it is missing the import of a wrapper succeeds but
@@ -65,6 +66,8 @@ SIGNATURES = {
     "g9_moe_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i64, _int, _vp]),
     "g9_moe_kernel_name": (ctypes.c_char_p, [_int, _int]),
+    "g9_fmha_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                           ctypes.c_float, _int, _int, _int, _vp]),
     "g9_workspace_size": (_sz, [_int, _i64, _i64, _i64, _int, _int]),
     "g9_workspace_init": (_int, [_vp, _sz, _vp]),
     "g9_workspace_error": (_int, [_vp, _sz, _vp, ctypes.POINTER(_int)]),

@@ -14,6 +14,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -23,7 +24,7 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 # The same kernels with per-workgroup phase stamps (-DG9_TIMING), for
 # profiling.py; never loaded by the wrappers unless G9_LIBRARY points at it.
 LIB_TIMING_PATH = os.path.join(PKG_DIR, "libg9gemm_timing.so")
-SOURCES = ["g9_capi.hip"]
+SOURCES = ["g9_capi.hip", "g9_fmha.hip"]  # GEMM + MoE + C ABI; flash-attention forward
 HEADERS = ["g9_common.hpp", "g9_gemm.hpp"]
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_*_f32, whose results
@@ -59,25 +60,39 @@ def build(verbose: bool = False, timing: bool = False) -> str:
 
     from . import isa_check
 
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
     lib_path = LIB_TIMING_PATH if timing else LIB_PATH
     flags = HIPCC_FLAGS + (["-DG9_TIMING"] if timing else [])
     tmp = lib_path + ".tmp"
     with tempfile.TemporaryDirectory(prefix="g9build") as work:
-        # -save-temps keeps the device assembly (in the scratch directory)
-        # without a second compilation.
-        cmd = [hipcc_path(), *flags, "-save-temps", "-I", os.path.join(REPO_DIR, "include"), *srcs, "-o", tmp]
-        if verbose:
-            print(" ".join(cmd), flush=True)
+        # Each source compiles to an object in a directory of its own, in
+        # parallel; -save-temps keeps its device assembly there without a
+        # second compilation.
+        def compile_one(src: str) -> tuple[str, str]:
+            d = os.path.join(work, os.path.splitext(src)[0])
+            os.makedirs(d)
+            obj = os.path.join(d, src + ".o")
+            cmd = [hipcc_path(), *[f for f in flags if f != "-shared"], "-c", "-save-temps", "-I",
+                   os.path.join(REPO_DIR, "include"), os.path.join(CSRC, src), "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            res = subprocess.run(cmd, capture_output=True, text=True, cwd=d)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {src} ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+            asm = [os.path.join(d, f) for f in os.listdir(d) if f.endswith("gfx950.s")]
+            if len(asm) != 1:
+                raise RuntimeError(f"expected one device assembly file for {src}, found {asm}")
+            return obj, asm[0]
+
+        with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+            built = list(pool.map(compile_one, SOURCES))
+        cmd = [hipcc_path(), *flags, *[o for o, _ in built], "-o", tmp]
         res = subprocess.run(cmd, capture_output=True, text=True, cwd=work)
         if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-        asm = [f for f in os.listdir(work) if f.endswith("gfx950.s")]
-        if len(asm) != len(SOURCES):
-            raise RuntimeError(f"expected {len(SOURCES)} device assembly file(s), found {asm}")
+            raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        asm = [a for _, a in built]
         bad, resources = [], []
         for f in asm:
-            with open(os.path.join(work, f)) as fh:
+            with open(f) as fh:
                 text = fh.read()
             bad += isa_check.check_text(text)
             resources += isa_check.resource_table(text)

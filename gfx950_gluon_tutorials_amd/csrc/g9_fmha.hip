@@ -1,0 +1,374 @@
+// Flash-attention forward (non-causal) for gfx950: O = softmax(Q K^T * sm_scale) V
+// per (batch, query head), with grouped K/V heads (query head h reads K/V head
+// h * HK / HQ).  Head dim 128, FP16 or BF16 in and out, fp32 softmax and
+// accumulation.  extern "C" entry: g9_fmha_fwd (include/gfx950_fmha.h).
+//
+// One workgroup owns 256 query rows of one (batch, head) and walks all keys in
+// tiles of 64.  Its 8 waves (2 per SIMD) own 32 query rows each, so every
+// row-wise reduction stays inside a wave.  Per key tile a wave runs
+//   S^T = K . Q^T    16 MFMAs 32x32x16 (two 32-key blocks x 8 steps of 16 d);
+//                    K fragments from LDS, Q fragments in registers;
+//   online softmax   running max m and (lane-partial) sum l in log2 units;
+//   O^T += V^T . P^T 16 MFMAs (4 blocks of 32 d x 4 steps of 16 keys);
+//                    P^T straight from the S^T registers, V^T through LDS
+//                    transpose reads.
+// The scores are computed transposed (the keys are the MFMA's rows): lane l
+// then holds 32 keys of query l % 32 (16 per 32-key block), so the row max and
+// the row sum of a query are in-lane reductions plus one exchange with lane
+// l ^ 32, the accumulator rescale is one per-lane factor, and the score
+// registers are already the B operand of the PV MFMA once its 16-key steps use
+// the key order the score layout gives each lane half: step t, lane half h,
+// slot u covers key 16t + 8(u / 4) + 4h + (u % 4).  V is read in that key order
+// with ds_read_b64_tr_b16, which within each 16-lane group gives lane 4a + b
+// element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12
+// (measured on gfx950): 4 keys of one head-dim column per read.
+//
+// K and V tiles (64 rows x 256 bytes) are double buffered in LDS and filled by
+// LDS-DMA.  The 16-byte chunk c of row r sits at chunk slot c ^ swz(r & 15),
+// which keeps the 16-row K reads and the 4-row V transpose reads free of bank
+// conflicts; the DMA applies it on the global side (each lane fetches the
+// chunk that belongs in its LDS slot).
+#include <stdint.h>
+
+#include "../../include/gfx950_fmha.h"
+#include "g9_common.hpp"
+
+namespace g9 {
+namespace fa {
+
+constexpr int kBlockM = 256;                // query rows per workgroup
+constexpr int kBlockN = 64;                 // keys per tile
+constexpr int kHd = 128;                    // head dim
+constexpr int kRowBytes = kHd * 2;          // one K/V row (256 bytes)
+constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile (16 KiB)
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazyThreshold = 8.f;       // log2 units: p < 256 between rescales
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+struct FaParams {
+  const char* q;
+  const char* k;
+  const char* v;
+  char* o;
+  float* lse;                        // [B][HQ][S] fp32, or null
+  long long q_b, q_h, k_b, k_h, v_b, v_h, o_b, o_h;  // batch / head strides, bytes
+  u32 ldq, ldk, ldv, ldo;            // sequence strides, bytes
+  int B, HQ, HK, S;
+  int mblocks;                       // ceil(S / 256)
+  int num_xcds;
+  float scale_log2;                  // sm_scale * log2(e)
+  int scale_on_q;                    // fold scale_log2 into Q (rounded to 16 bit) before the loop
+};
+
+// Chunk swizzle of row r (a bijection of 0..15): 16 consecutive rows get 16
+// distinct values, and 4 consecutive rows from a multiple of 4 get distinct
+// bits 1-2, so the K reads (16 rows, one chunk) and the V transpose reads (4
+// rows, one 32-byte chunk pair) both cover distinct banks.
+G9_DEV int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8); }
+
+// MFMA 32x32x16 on 16-bit operands given as raw registers.
+template <bool BF16>
+G9_DEV f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
+// Two fp32 values -> one register of two 16-bit values (round to nearest even).
+template <bool BF16>
+G9_DEV u32 pack2(float x, float y) {
+  if constexpr (BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(u32, __builtin_convertvector((f32x2){x, y}, b2));
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(u32, __builtin_convertvector((f32x2){x, y}, h2));
+  }
+}
+
+// Two 16-bit values of one register -> fp32.
+template <bool BF16>
+G9_DEV f32x2 unpack2(u32 w) {
+  if constexpr (BF16) {
+    return f32x2{__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_convertvector(__builtin_bit_cast(h2, w), f32x2);
+  }
+}
+
+// Value of lane l ^ 32 combined with this lane's by a symmetric op.
+template <class F>
+G9_DEV float xhalf(float x, F op) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return op(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+G9_DEV u32x2 tr_read(u32 addr) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((G9_LDS s16x4*)(uintptr_t)addr);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+template <bool BF16, bool LAZY>
+G9_DEV void fmha_fwd(const FaParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
+  // Workgroups of one (batch, head) run consecutively on one XCD, so its L2
+  // serves their shared K and V.
+  const int total = p.B * p.HQ * p.mblocks;
+  int pid, unused;
+  tile_coords(blockIdx.x, total, total, 1, p.num_xcds, 1, pid, unused);
+  const int bh = pid / p.mblocks, mb = pid - bh * p.mblocks;
+  const int b = bh / p.HQ, hq = bh - b * p.HQ;
+  const int hk = hq * p.HK / p.HQ;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5;  // lane half
+  const int nt = p.S / kBlockN;
+  const u32 lds0 = (u32)(uintptr_t)to_lds(smem);
+
+  const char* qb = p.q + b * p.q_b + hq * p.q_h;
+  const char* kb = p.k + b * p.k_b + hk * p.k_h;
+  const char* vb = p.v + b * p.v_b + hk * p.v_h;
+  const rsrc_t rq = make_rsrc(qb, (u32)p.S * p.ldq);
+  const rsrc_t rk = make_rsrc(kb, (u32)p.S * p.ldk);
+  const rsrc_t rv = make_rsrc(vb, (u32)p.S * p.ldv);
+
+  // Q fragments (B operand of S^T = K Q^T): lane l holds Q[q][16s + 8h .. + 7]
+  // of query q = row0 + l % 32, for s = 0..7.  Rows past S read zero.
+  const int qrow = mb * kBlockM + wave * 32 + (lane & 31);
+  u32x4 qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (u32)qrow * p.ldq + (16 * s + 8 * h) * 2, 0, 0));
+  // With scale_on_q the scores come out of the MFMA already in log2 units.
+  float sc = p.scale_log2;
+  if (p.scale_on_q) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f32x2 x = unpack2<BF16>(qf[s][e]);
+        qf[s][e] = pack2<BF16>(x.x * sc, x.y * sc);
+      }
+    sc = 1.f;
+  }
+
+  // DMA of one K or V tile: wave w fills rows 8w..8w+7 with two 16-byte DMAs
+  // of 4 rows each; lane i fetches the chunk that belongs in LDS slot i.
+  u32 voffk[2], voffv[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = 8 * wave + 4 * t + (lane >> 4);
+    const int ch = (lane & 15) ^ swz(row & 15);
+    voffk[t] = (u32)row * p.ldk + ch * 16;
+    voffv[t] = (u32)row * p.ldv + ch * 16;
+  }
+  auto issue = [&](int tile, int buf) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const u32 dst = lds0 + buf * kTileBytes + (8 * wave + 4 * t) * kRowBytes;
+      dma16(rk, (G9_LDS void*)(uintptr_t)dst, voffk[t], (u32)tile * kBlockN * p.ldk);
+      dma16(rv, (G9_LDS void*)(uintptr_t)(dst + 2 * kTileBytes), voffv[t], (u32)tile * kBlockN * p.ldv);
+    }
+  };
+  issue(0, 0);
+  if (nt > 1) issue(1, 1);
+
+  // LDS read addresses (relative to the buffer).  K: lane l reads row l % 32
+  // (+32 per block), chunk 2s + h.  V: lane 16G + j reads row 4(G/2) + j/4
+  // (+8 for the second read, +16 per step), 8 bytes at head-dim column
+  // 32 dblk + 16(G % 2) + 4(j % 4).
+  u32 ak[8], av[4][2];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) ak[s] = (u32)(lane & 31) * kRowBytes + (((2 * s + h) ^ swz(lane & 15)) << 4);
+  {
+    const int G = lane >> 4, j = lane & 15;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int sec = 0; sec < 2; ++sec) {
+        const int row = 4 * (G >> 1) + (j >> 2) + 8 * sec;
+        const int ch = 4 * dblk + 2 * (G & 1) + ((j & 3) >> 1);
+        av[dblk][sec] = (u32)row * kRowBytes + ((ch ^ swz(row & 15)) << 4) + 8 * (j & 1);
+      }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
+  float m = -__builtin_inff(), l = 0.f;
+
+  for (int j = 0; j < nt; ++j) {
+    const u32 kbuf = lds0 + (j & 1) * kTileBytes;
+    const u32 vbuf = kbuf + 2 * kTileBytes;
+    // Tile j's DMAs (all waves') landed; tile j + 1's may still be in flight.
+    if (j + 1 < nt)
+      waitcnt<4, 15>();
+    else
+      waitcnt<0, 15>();
+    barrier();
+
+    f32x16 s0 = {}, s1 = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 k0 = *(const G9_LDS u32x4*)(uintptr_t)(kbuf + ak[s]);
+      const u32x4 k1 = *(const G9_LDS u32x4*)(uintptr_t)(kbuf + ak[s] + 32 * kRowBytes);
+      s0 = mfma<BF16>(k0, qf[s], s0);
+      s1 = mfma<BF16>(k1, qf[s], s1);
+    }
+
+    // Online softmax in log2 units: x = s * sm_scale * log2(e).  LAZY keeps
+    // the running max unless the tile's max exceeds it by more than
+    // kLazyThreshold (p then stays below 2^kLazyThreshold; o and l share the
+    // stale frame, so o / l is unchanged) and skips the rescale of o when no
+    // row of the wave moved.
+    float mx = s0[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, s0[i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, s1[i]);
+    mx = xhalf(mx, [](float a, float c) { return __builtin_fmaxf(a, c); });
+    const float mt = mx * sc;
+    const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], sc, -m_new));
+      s1[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], sc, -m_new));
+      rs += s0[i] + s1[i];
+    }
+    l = l * alpha + rs;
+    m = m_new;
+    if (!LAZY || __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+    }
+
+    // P^T fragments: step t, slot u = score register 8(t % 2) + u of block t / 2.
+    u32x4 pf[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f32x16& sv = t < 2 ? s0 : s1;
+      const int r0 = 8 * (t & 1);
+      pf[t] = u32x4{pack2<BF16>(sv[r0 + 0], sv[r0 + 1]), pack2<BF16>(sv[r0 + 2], sv[r0 + 3]),
+                    pack2<BF16>(sv[r0 + 4], sv[r0 + 5]), pack2<BF16>(sv[r0 + 6], sv[r0 + 7])};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const u32x2 lo = tr_read(vbuf + av[d][0] + t * 16 * kRowBytes);
+        const u32x2 hi = tr_read(vbuf + av[d][1] + t * 16 * kRowBytes);
+        o[d] = mfma<BF16>(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[t], o[d]);
+      }
+
+    // Every wave done with this buffer before it is refilled with tile j + 2.
+    waitcnt<63, 0>();
+    barrier();
+    if (j + 2 < nt) issue(j + 2, j & 1);
+  }
+
+  // Normalise, store O (lane l: query row0 + l % 32, head-dim columns
+  // 32 dblk + 8r + 4h .. + 3 of register quad r) and the log-sum-exp.
+  const float lt = xhalf(l, [](float a, float c) { return a + c; });
+  const float inv = 1.f / lt;
+  if (qrow < p.S) {
+    char* orow = p.o + b * p.o_b + hq * p.o_h + (size_t)qrow * p.ldo;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = 32 * d + 8 * r + 4 * h;
+        const u32x2 w = {pack2<BF16>(o[d][4 * r] * inv, o[d][4 * r + 1] * inv),
+                         pack2<BF16>(o[d][4 * r + 2] * inv, o[d][4 * r + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + col * 2) = w;
+      }
+    if (p.lse && h == 0) p.lse[((size_t)b * p.HQ + hq) * p.S + qrow] = (m + __builtin_log2f(lt)) * kLn2;
+  }
+}
+
+}  // namespace fa
+}  // namespace g9
+
+using namespace g9;
+
+// Kernels: g9_fmha_fwd_{bf16,f16}_v{3,4}; v3 rescales every tile, v4 lazily.
+#define G9_FMHA_KERNEL(NAME, BF16, LAZY)                                                                   \
+  extern "C" __global__ __launch_bounds__(fa::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void \
+  NAME(fa::FaParams p) {                                                                                  \
+    fa::fmha_fwd<BF16, LAZY>(p);                                                                          \
+  }
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false)
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v4, true, true)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v4, false, true)
+
+extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t HQ,
+                           int64_t HK, int64_t S, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* o_strides, float sm_scale, int dtype,
+                           int scale_on_q, int variant, void* stream) {
+  if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
+  if (variant != 3 && variant != 4) return G9_ERR_SCHEDULE;
+  if (B <= 0 || HQ <= 0 || HK <= 0 || S <= 0 || HQ % HK != 0) return G9_ERR_SHAPE;
+  if (D != fa::kHd || S % fa::kBlockN != 0) return G9_ERR_SHAPE;
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return G9_ERR_LAYOUT;
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  const void* ptr[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    // (batch, head, seq, dim) strides in elements: unit head-dim stride,
+    // 16-byte aligned rows, and every row offset of a (batch, head) slice,
+    // including a 256-row tile past the end, inside 31 bits.
+    if (st[i][3] != 1 || st[i][2] < D || (st[i][2] * 2) % 16 != 0 || st[i][0] < 0 || st[i][1] < 0) return G9_ERR_LAYOUT;
+    if ((uintptr_t)ptr[i] % 16 != 0 || (st[i][0] * 2) % 16 != 0 || (st[i][1] * 2) % 16 != 0) return G9_ERR_LAYOUT;
+    if ((S + fa::kBlockM) * st[i][2] * 2 >= (int64_t(1) << 31)) return G9_ERR_SHAPE;
+  }
+  if (lse && (uintptr_t)lse % 4 != 0) return G9_ERR_LAYOUT;
+  const int64_t mblocks = (S + fa::kBlockM - 1) / fa::kBlockM;
+  if (B * HQ * mblocks > INT32_MAX) return G9_ERR_SHAPE;
+  if (!(sm_scale > 0.f)) return G9_ERR_SHAPE;
+  fa::FaParams p{};
+  p.q = static_cast<const char*>(q);
+  p.k = static_cast<const char*>(k);
+  p.v = static_cast<const char*>(v);
+  p.o = static_cast<char*>(o);
+  p.lse = lse;
+  p.q_b = q_strides[0] * 2;
+  p.q_h = q_strides[1] * 2;
+  p.k_b = k_strides[0] * 2;
+  p.k_h = k_strides[1] * 2;
+  p.v_b = v_strides[0] * 2;
+  p.v_h = v_strides[1] * 2;
+  p.o_b = o_strides[0] * 2;
+  p.o_h = o_strides[1] * 2;
+  p.ldq = (u32)(q_strides[2] * 2);
+  p.ldk = (u32)(k_strides[2] * 2);
+  p.ldv = (u32)(v_strides[2] * 2);
+  p.ldo = (u32)(o_strides[2] * 2);
+  p.B = (int)B;
+  p.HQ = (int)HQ;
+  p.HK = (int)HK;
+  p.S = (int)S;
+  p.mblocks = (int)mblocks;
+  p.num_xcds = 8;
+  p.scale_log2 = sm_scale * fa::kLog2e;
+  p.scale_on_q = scale_on_q != 0;
+  void* args[] = {&p};
+  const bool bf = dtype == G9_BF16, lazy = variant == 4;
+  const void* fn = lazy ? (bf ? reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v4)
+                              : reinterpret_cast<const void*>(g9_fmha_fwd_f16_v4))
+                        : (bf ? reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v3)
+                              : reinterpret_cast<const void*>(g9_fmha_fwd_f16_v3));
+  return hipLaunchKernel(fn, dim3((unsigned)(B * HQ * mblocks)), dim3(fa::kThreads), args, 0,
+                         reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}

@@ -1,5 +1,5 @@
 """CPU checks of the C ABI: the built library loads, exports exactly the
-entry points include/gfx950_gemm.h declares, and rejects bad arguments with
+entry points include/gfx950_gemm.h and include/gfx950_fmha.h declare, and rejects bad arguments with
 the documented status codes before touching the GPU (no launches here)."""
 
 import ctypes
@@ -11,11 +11,12 @@ import pytest
 from gfx950_gluon_tutorials_amd import _lib
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "gfx950_gemm.h")
+FMHA_HEADER = os.path.join(os.path.dirname(HEADER), "gfx950_fmha.h")
 FAKE = 0x10000  # 16-byte aligned non-null address; never dereferenced on these paths
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = open(HEADER).read() + open(FMHA_HEADER).read()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(g9_\w+)\s*\(", text, flags=re.M)))
 
 
@@ -24,7 +25,7 @@ def test_library_exports_every_declared_function():
     names = declared_functions()
     assert names == sorted(_lib.SIGNATURES), "binding table out of sync with the header"
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in gfx950_gemm.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in a header but not exported"
 
 
 TIMING_HEADER = os.path.join(os.path.dirname(HEADER), "gfx950_gemm_timing.h")
