@@ -105,11 +105,50 @@ G9_DEV f32x2 unpack2(u32 w) {
   }
 }
 
+// acc + the two 16-bit values of w (fp32 accumulate).
+template <bool BF16>
+G9_DEV float dot2_ones(u32 w, float acc) {
+  if constexpr (BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, w), __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), __builtin_bit_cast(h2, 0x3c003c00u), acc, false);
+  }
+}
+
 // Value of lane l ^ 32 combined with this lane's by a symmetric op.
 template <class F>
 G9_DEV float xhalf(float x, F op) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
   return op(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+// LDS-DMA of 16 bytes per lane (lane i writes lds + 16 i, reading global
+// voff + soff) issued as inline assembly, so the compiler does not track it:
+// it adds no wait for these DMAs before LDS reads (it cannot tell the read
+// addresses from the DMA targets apart and would wait for every DMA in
+// flight).  The caller orders them with explicit vmcnt waits and barriers.
+// M0 is written here; nothing else in these kernels uses it.
+G9_DEV void dma16_untracked(rsrc_t r, u32 lds, u32 voff, u32 soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r), "s"(soff)
+               : "memory");
+}
+
+// Pins a value to this point of the program: the compiler can neither move
+// its computation past the statement nor sink it toward its uses.
+G9_DEV void pin(float& x) { asm volatile("" : "+v"(x)); }
+G9_DEV void pin(u32& x) { asm volatile("" : "+v"(x)); }
+template <class V>
+G9_DEV void pin_vec(V& v) {
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(V) / 4); ++i) {
+    float x = v[i];
+    pin(x);
+    v[i] = x;
+  }
 }
 
 G9_DEV u32x2 tr_read(u32 addr) {
@@ -296,16 +335,381 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined form.  Each wave's loop over key tiles j is cut into four
+// clusters, each closed by a workgroup barrier:
+//   D1(j)  QK MFMAs of tile j+1 (K_{j+1} from registers) and, in their issue
+//          shadow, the second half of tile j's softmax (the remaining
+//          exponentials, P_j to 16 bit, the row sum);
+//   M1(j)  LDS reads of V_j; DMA of K_{j+3};
+//   D2(j)  PV MFMAs of tile j and, in their shadow, the first half of tile
+//          j+1's softmax (row max, new running max, most exponentials);
+//   M2(j)  LDS reads of K_{j+2}; DMA of V_{j+2}; rescale of O and l.
+// Waves 4-7 run one cluster behind waves 0-3, so on every SIMD one wave is in
+// a dot cluster (MFMA + VALU) while the other is in a memory cluster: the
+// matrix pipe, the VALU and the LDS / memory pipe are busy at the same time.
+// K and V tiles are double buffered in LDS (tile t in buffer t & 1); each DMA
+// is waited for (by its own wave, then a barrier) one cluster before the tile
+// is read, which gives it about one and a half loop iterations to land.
+//
+// LDS tiles are stored column-major in 16-byte chunks: chunk c (head-dim
+// values 8c..8c+7) of all 64 rows is one contiguous KiB (one DMA: lane i
+// fetches row i), chunk columns kPitchK / kPitchV bytes apart.  Every LDS read
+// address is then one per-lane base register plus an immediate: K reads
+// (row = lane % 32 (+32), chunk 2s + lane / 32) cover 256 contiguous bytes per
+// 16 lanes; a V transpose read of 16 lanes covers 4 rows of two adjacent
+// chunks, 64 bytes each, which the 64-byte pad of kPitchV puts on distinct
+// banks.
+// ---------------------------------------------------------------------------
+
+#ifndef G9_FMHA_VN1
+#define G9_FMHA_VN1 4  // VALU instructions after each QK MFMA of D1
+#endif
+#ifndef G9_FMHA_VN2
+#define G9_FMHA_VN2 4  // VALU instructions after each PV MFMA of D2
+#endif
+#ifndef G9_FMHA_VEC1_EXPS
+#define G9_FMHA_VEC1_EXPS 20  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
+#endif
+
+constexpr int kPitchK = 1024;                  // bytes between K chunk columns
+constexpr int kPitchV = 1088;                  // bytes between V chunk columns
+constexpr int kTileK = 16 * kPitchK;           // one K tile in LDS
+constexpr int kTileV = 16 * kPitchV;           // one V tile in LDS
+constexpr int kLdsV = 2 * kTileK;              // V buffers after the two K buffers
+constexpr int kLdsBytes = 2 * kTileK + 2 * kTileV;
+
+template <bool BF16, bool LAZY>
+struct Pipe {
+  static constexpr int kE1 = G9_FMHA_VEC1_EXPS;
+  const FaParams& p;
+  int nt, nte, wave;  // tiles, tiles rounded up to even, wave index
+  u32 lds0;
+  rsrc_t rk, rv;
+  u32 voffk, voffv;  // lane's row offset in global K / V
+  u32 ak, av;        // lane's LDS read base for K / V
+  float sc;
+  u32x4 qf[8];
+  u32x4 kv[16];  // K_t (kv[2s + blk]: step s of 16 head-dim values, key block blk) or V_t (kv[4t + d])
+  f32x16 o[4];   // O^T, head-dim block d
+  float m, l, alpha;
+
+  G9_DEV explicit Pipe(const FaParams& pp) : p(pp) {}
+
+  // Wave w fetches chunk columns 2w and 2w + 1 of a tile.
+  G9_DEV void dma_k(int tile, int buf) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      dma16_untracked(rk, lds0 + buf * kTileK + (2 * wave + c) * kPitchK, voffk,
+                      (u32)tile * kBlockN * p.ldk + (2 * wave + c) * 16);
+  }
+  G9_DEV void dma_v(int tile, int buf) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      dma16_untracked(rv, lds0 + kLdsV + buf * kTileV + (2 * wave + c) * kPitchV, voffv,
+                      (u32)tile * kBlockN * p.ldv + (2 * wave + c) * 16);
+  }
+  template <int BUF>
+  G9_DEV void read_k() {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+        kv[2 * s + blk] = *(const G9_LDS u32x4*)(uintptr_t)(ak + BUF * kTileK + 2 * s * kPitchK + blk * 512);
+  }
+  template <int BUF>
+  G9_DEV void read_v() {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const u32 a = av + BUF * kTileV + 4 * d * kPitchV + 256 * t;
+        const u32x2 lo = tr_read(a);
+        const u32x2 hi = tr_read(a + 128);
+        kv[4 * t + d] = u32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+  }
+  // S^T of the tile in kv: two 32-key blocks.
+  G9_DEV void qk(f32x16& s0, f32x16& s1) {
+    s0 = mfma<BF16>(kv[0], qf[0], f32x16{});
+    s1 = mfma<BF16>(kv[1], qf[0], f32x16{});
+#pragma unroll
+    for (int s = 1; s < 8; ++s) {
+      s0 = mfma<BF16>(kv[2 * s], qf[s], s0);
+      s1 = mfma<BF16>(kv[2 * s + 1], qf[s], s1);
+    }
+  }
+  // O^T += V^T P^T; P in 16 bit as vec2 left it in (s0, s1).
+  G9_DEV void pv(const f32x16& s0, const f32x16& s1) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f32x16& sv = t < 2 ? s0 : s1;
+      const u32x4 pt = t & 1 ? __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 8, 9, 10, 11))
+                             : __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 0, 1, 2, 3));
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] = mfma<BF16>(kv[4 * t + d], pt, o[d]);
+    }
+  }
+  // p = 2^(x * sc - m) for score register i (0..31) of a lane: block i / 16,
+  // register i % 16.
+  G9_DEV void expo(f32x16& s0, f32x16& s1, int i) const {
+    if (i < 16)
+      s0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], sc, -m));
+    else
+      s1[i - 16] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i - 16], sc, -m));
+  }
+
+  // First half of a tile's softmax: row max, running max, alpha, and the
+  // first kE1 exponentials (in place).
+  G9_DEV void vec1(f32x16& s0, f32x16& s1) {
+    float a = __builtin_fmaxf(__builtin_fmaxf(s0[0], s0[1]), s0[2]);
+    float b = __builtin_fmaxf(__builtin_fmaxf(s0[8], s0[9]), s0[10]);
+    float c = __builtin_fmaxf(__builtin_fmaxf(s1[0], s1[1]), s1[2]);
+    float d = __builtin_fmaxf(__builtin_fmaxf(s1[8], s1[9]), s1[10]);
+#pragma unroll
+    for (int i = 3; i < 8; i += 2) {
+      const int i1 = i + 1 < 8 ? i + 1 : i;
+      a = __builtin_fmaxf(__builtin_fmaxf(a, s0[i]), s0[i1]);
+      b = __builtin_fmaxf(__builtin_fmaxf(b, s0[8 + i]), s0[8 + i1]);
+      c = __builtin_fmaxf(__builtin_fmaxf(c, s1[i]), s1[i1]);
+      d = __builtin_fmaxf(__builtin_fmaxf(d, s1[8 + i]), s1[8 + i1]);
+    }
+    float mx = __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+    mx = xhalf(mx, [](float x, float y) { return __builtin_fmaxf(x, y); });
+    const float mt = mx * sc;
+    const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
+    alpha = __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+#pragma unroll
+    for (int i = 0; i < kE1; ++i) expo(s0, s1, i);
+  }
+  // Second half: the remaining exponentials, P to 16 bit, l += row sum (of
+  // the rounded values, which is what the PV MFMAs weight V with).  The
+  // 16-bit pairs of PV step t are written over the first four registers of
+  // their eight scores (registers 8(t % 2) .. +3 of block t / 2), so P needs
+  // no registers of its own.
+  G9_DEV void vec2(f32x16& s0, f32x16& s1) {
+#pragma unroll
+    for (int i = kE1; i < 32; ++i) expo(s0, s1, i);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f32x16& sv = t < 2 ? s0 : s1;
+      const int r0 = 8 * (t & 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[r0 + e] = __uint_as_float(pack2<BF16>(sv[r0 + 2 * e], sv[r0 + 2 * e + 1]));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) l = dot2_ones<BF16>(__float_as_uint((t < 2 ? s0 : s1)[8 * (t & 1) + e]), l);
+  }
+  // Pins the 16-bit P pairs and l (vec2's results).
+  G9_DEV void pin_p(f32x16& s0, f32x16& s1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = s0[e], b = s0[8 + e], c = s1[e], d = s1[8 + e];
+      pin(a), pin(b), pin(c), pin(d);
+      s0[e] = a, s0[8 + e] = b, s1[e] = c, s1[8 + e] = d;
+    }
+    pin(l);
+  }
+  G9_DEV void rescale() {
+    l *= alpha;
+    if (!LAZY || __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+    }
+  }
+
+  // Interleave of a dot cluster: MFMA i followed by VN VALU instructions.
+  template <int VN>
+  G9_DEV static void interleave() {
+#ifndef G9_FMHA_NO_INTERLEAVE
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VALU, VN, 0);
+    }
+#endif
+  }
+
+  // One loop iteration; PAR = j & 1 fixes the LDS buffers; (c0, c1) hold
+  // tile j's scores after vec1, (n0, n1) receive tile j+1's; NEXT: tile j+1
+  // exists.  The loop runs over an even number of tiles nte: when nt is odd
+  // the last tile is a phantom past the end of the sequence (its DMAs read
+  // zeros from the buffer range check) whose scores are set to -inf, so it
+  // adds nothing.  Registers are written unconditionally (a read past the
+  // last tile reads a stale but in-bounds buffer), so no value has to survive
+  // a skipped branch.
+  template <int PAR, bool NEXT>
+  G9_DEV void step(int j, f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+    // D1(j)
+    if constexpr (NEXT) {
+      qk(n0, n1);
+      vec2(c0, c1);
+      interleave<G9_FMHA_VN1>();
+      pin_vec(n0);
+      pin_vec(n1);
+    } else {
+      vec2(c0, c1);
+    }
+    pin_p(c0, c1);
+    barrier();
+    // M1(j): V_j was waited for at the end of M2(j-1) (or the prologue).
+    read_v<PAR>();
+    if (j + 2 < nte) waitcnt<2, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
+    if (j + 3 < nte) dma_k(j + 3, PAR ^ 1);
+    if constexpr (NEXT) {
+      if (j + 1 >= nt) {  // the phantom tile (a branch, not 32 selects per step)
+        asm volatile("");
+        n0 = f32x16{} - __builtin_inff();
+        n1 = n0;
+      }
+    }
+    waitcnt<63, 0>();
+    barrier();
+    // D2(j)
+    if constexpr (NEXT) {
+      pv(c0, c1);
+      vec1(n0, n1);
+      interleave<G9_FMHA_VN2>();
+      pin_vec(n0);
+      pin_vec(n1);
+      pin(m);
+      pin(alpha);
+    } else {
+      pv(c0, c1);
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) pin_vec(o[d]);
+    barrier();
+    // M2(j)
+    if constexpr (NEXT) {
+      read_k<PAR>();
+      if (j + 3 < nte)
+        waitcnt<2, 15>();  // V_{j+1} landed (K_{j+3} may be in flight)
+      else
+        waitcnt<0, 15>();
+      rescale();
+    }
+    if (j + 2 < nte) dma_v(j + 2, PAR);
+    waitcnt<63, 0>();
+    barrier();
+  }
+};
+
+template <bool BF16, bool LAZY>
+G9_DEV void fmha_fwd_pp(const FaParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  const int total = p.B * p.HQ * p.mblocks;
+  int pid, unused;
+  tile_coords(blockIdx.x, total, total, 1, p.num_xcds, 1, pid, unused);
+  const int bh = pid / p.mblocks, mb = pid - bh * p.mblocks;
+  const int b = bh / p.HQ, hq = bh - b * p.HQ;
+  const int hk = hq * p.HK / p.HQ;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int h = lane >> 5;
+
+  Pipe<BF16, LAZY> P(p);
+  P.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  P.nt = p.S / kBlockN;
+  P.nte = (P.nt + 1) & ~1;
+  P.lds0 = (u32)(uintptr_t)to_lds(smem);
+  const int nte = P.nte, wave = P.wave;
+  const char* qb = p.q + b * p.q_b + hq * p.q_h;
+  const rsrc_t rq = make_rsrc(qb, (u32)p.S * p.ldq);
+  P.rk = make_rsrc(p.k + b * p.k_b + hk * p.k_h, (u32)p.S * p.ldk);
+  P.rv = make_rsrc(p.v + b * p.v_b + hk * p.v_h, (u32)p.S * p.ldv);
+
+  const int qrow = mb * kBlockM + wave * 32 + (lane & 31);
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    P.qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (u32)qrow * p.ldq + (16 * s + 8 * h) * 2, 0, 0));
+  P.voffk = (u32)lane * p.ldk;
+  P.voffv = (u32)lane * p.ldv;
+  P.ak = P.lds0 + h * kPitchK + (lane & 31) * 16;
+  {
+    const int G = lane >> 4, jj = lane & 15;
+    P.av = P.lds0 + kLdsV + (2 * (G & 1) + ((jj & 3) >> 1)) * kPitchV + (4 * (G >> 1) + (jj >> 2)) * 16 + 8 * (jj & 1);
+  }
+  // Prologue: K_0, V_0, K_1 in; S_0 and its first softmax half; K_2 and V_1
+  // requested (in that order: the loop expects K_{j+2} before V_{j+1}); K_1
+  // in registers.
+  P.dma_k(0, 0);
+  P.dma_v(0, 0);
+  P.dma_k(1, 1);
+  P.sc = p.scale_log2;
+  if (p.scale_on_q) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f32x2 x = unpack2<BF16>(P.qf[s][e]);
+        P.qf[s][e] = pack2<BF16>(x.x * P.sc, x.y * P.sc);
+      }
+    P.sc = 1.f;
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) P.o[d] = f32x16{};
+  P.m = -__builtin_inff();
+  P.l = 0.f;
+  waitcnt<0, 15>();
+  barrier();
+  P.template read_k<0>();
+  f32x16 sa0, sa1, sb0, sb1;
+  P.qk(sa0, sa1);
+  waitcnt<63, 0>();
+  barrier();  // every wave has read K_0: its buffer takes K_2
+  if (nte > 2) P.dma_k(2, 0);
+  P.dma_v(1, 1);
+  P.vec1(sa0, sa1);
+  P.l *= P.alpha;
+  P.template read_k<1>();
+  waitcnt<63, 0>();
+
+  const bool lag = wave >= 4;
+  if (lag) barrier();
+  int j = 0;
+  for (; j + 2 < nte; j += 2) {
+    P.template step<0, true>(j, sa0, sa1, sb0, sb1);
+    P.template step<1, true>(j + 1, sb0, sb1, sa0, sa1);
+  }
+  P.template step<0, true>(j, sa0, sa1, sb0, sb1);
+  P.template step<1, false>(j + 1, sb0, sb1, sa0, sa1);
+  if (!lag) barrier();
+
+  const float lt = xhalf(P.l, [](float x, float y) { return x + y; });
+  const float inv = 1.f / lt;
+  if (qrow < p.S) {
+    char* orow = p.o + b * p.o_b + hq * p.o_h + (size_t)qrow * p.ldo;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = 32 * d + 8 * r + 4 * h;
+        const u32x2 w = {pack2<BF16>(P.o[d][4 * r] * inv, P.o[d][4 * r + 1] * inv),
+                         pack2<BF16>(P.o[d][4 * r + 2] * inv, P.o[d][4 * r + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + col * 2) = w;
+      }
+    if (p.lse && h == 0) p.lse[((size_t)b * p.HQ + hq) * p.S + qrow] = (P.m + __builtin_log2f(lt)) * kLn2;
+  }
+}
+
 }  // namespace fa
 }  // namespace g9
 
 using namespace g9;
 
+#ifndef G9_FMHA_SIMPLE
+#define FMHA_IMPL fmha_fwd_pp
+#else
+#define FMHA_IMPL fmha_fwd
+#endif
 // Kernels: g9_fmha_fwd_{bf16,f16}_v{3,4}; v3 rescales every tile, v4 lazily.
 #define G9_FMHA_KERNEL(NAME, BF16, LAZY)                                                                   \
   extern "C" __global__ __launch_bounds__(fa::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void \
   NAME(fa::FaParams p) {                                                                                  \
-    fa::fmha_fwd<BF16, LAZY>(p);                                                                          \
+    fa::FMHA_IMPL<BF16, LAZY>(p);                                                                        \
   }
 G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false)
 G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false)
