@@ -17,8 +17,10 @@ The JSON line also carries the roofline of the dominant kernel (MFMA-bound:
 achieved TFLOP/s vs the published dense peak) with the HBM traffic per launch
 read from the committed rocprof counter summary when present, the other
 dtypes, the stream-K shapes, split-K against data-parallel on grids of 16-128
-tiles, the grouped (MoE) GEMMs, and a CPU baseline: the oracle's fp32 GEMM
-of the dequantized operands timed on this host on a bounded row sample.
+tiles, the grouped (MoE) GEMMs, the flash-attention forward (fmha_v4 and
+fmha_v3 at B=32 H=8 S=8192 D=128, bf16 and fp16, against the reference's
+published bf16 numbers), and a CPU baseline: torch.matmul in fp32 on the
+dequantized operands timed on this host on a bounded row sample.
 """
 
 from __future__ import annotations
@@ -46,6 +48,10 @@ REFERENCE_TFLOPS["bf16"] = 1696.0
 REFERENCE_TFLOPS_8W["bf16"] = 1573.6
 HEADLINE_K = {"bf8": (16384, 3476.0, 3131.1), "mxfp4": (32768, 5804.0, 5195.9), "mxfp4ps": (32768, 5804.0, None)}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+# Flash-attention forward: the reference's tuned shape and its published
+# numbers (bf16, kernels/attention/README.md:619-632; no fp16 figure).
+FMHA_SHAPE = {"B": 32, "H": 8, "S": 8192, "D": 128}
+FMHA_REFERENCE_TFLOPS = {("bf16", 4): 1261.0, ("bf16", 3): 1189.0}
 
 
 def parse_args():
@@ -68,6 +74,11 @@ def parse_args():
     p.add_argument("--vendor", type=int, default=1,
                    help="also time ROCm's hipBLASLt (torch.matmul / torch._scaled_mm) on the same shapes, "
                         "interleaved with ours, for fp16/bf16/bf8 at K=8192 (0/1)")
+    p.add_argument("--fmha", type=int, default=1,
+                   help="also time the flash-attention forward at B=32 H=8 S=8192 D=128 (0/1)")
+    p.add_argument("--fmha-only", type=int, default=0,
+                   help="time only the flash-attention forward (--steps / --warmup / --settle-ms launches of each "
+                        "case) and print its object (for profilers)")
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--serialized", type=int, default=0,
@@ -562,6 +573,48 @@ def make_vendor_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: 
     return launch
 
 
+def fmha_bench(args, dev) -> dict:
+    """Flash-attention forward (g9_fmha_fwd through run_gluon_attention), bhsd,
+    non-causal, fmha_v4 (lazy rescale) and fmha_v3 (eager), bf16 and fp16, at
+    FMHA_SHAPE.  One (q, k, v, o) set is 2 GiB, far beyond the caches, so no
+    rotation (the reference's rotating_set_count gives 1 for this shape,
+    kernels/attention/bench.py:186-199).  FLOPs: 4 B H S^2 D
+    (kernels/attention/common.py:177-184)."""
+    import torch
+
+    from gfx950_gluon_tutorials_amd.attention import MetaData, compute_flops, fmha_v3, fmha_v4
+
+    B, H, S, D = (FMHA_SHAPE[k] for k in ("B", "H", "S", "D"))
+    flop = compute_flops(B, H, S, S, D, False)
+    out = {}
+    for dt, tdt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+        g = torch.Generator(device=dev).manual_seed(20)
+        q, k, v = (torch.randn(B, H, S, D, device=dev, dtype=tdt, generator=g) for _ in range(3))
+        o = torch.empty_like(q)
+        md = MetaData(sm_scale=D**-0.5)
+        md.max_seqlens_q = md.max_seqlens_k = S
+        md.layout = "bhsd"
+        for variant, fn in ((4, fmha_v4.run_gluon_attention), (3, fmha_v3.run_gluon_attention)):
+            def launch(i, schedule="dp", fn=fn):
+                fn(q, k, v, o, md)
+
+            if args.fmha_only:
+                ms = time_case(launch, args.steps, args.warmup, settle_s=args.settle_ms / 1e3)
+            else:
+                ms = time_case(launch, max(10, args.steps // 10), max(3, args.warmup // 20), settle_s=args.settle_ms / 2e3)
+            tf = flop / (ms * 1e-3) / 1e12
+            ref = FMHA_REFERENCE_TFLOPS.get((dt, variant))
+            key = f"{dt}_v{variant}"
+            out[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
+                        "reference_tflops": ref, "vs_reference": round(tf / ref, 4) if ref else None}
+            print(f"# fmha_v{variant} {dt} B={B} H={H} S={S} D={D}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  "
+                  f"{100 * tf / PEAK[dt]:.1f}% of peak" + (f"  | reference {ref:.0f}" if ref else ""), flush=True)
+        del q, k, v, o
+        torch.cuda.empty_cache()
+    out["shape"] = dict(FMHA_SHAPE, layout="bhsd", causal=False)
+    return out
+
+
 def moe_set_bytes(dtype: str) -> int:
     E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
     if dtype == "fp16":
@@ -608,6 +661,9 @@ def main():
             lib(i)
         torch.cuda.synchronize()
         print(f"# pair: {args.pair} launches each of ours and hipBLASLt ({dt})", flush=True)
+        return
+    if args.fmha_only:
+        print(json.dumps({"fmha": fmha_bench(args, dev)}), flush=True)
         return
     dtypes = [d for d in args.dtypes.split(",") if d]
     if args.only:
@@ -735,6 +791,7 @@ def main():
                   f"(256-row tiles {100 * T / padded:.1f}% filled)", flush=True)
             del launch
             torch.cuda.empty_cache()
+    fmha = fmha_bench(args, dev) if args.fmha and not args.only else {}
     if args.copy_mb:
         copy_calibration(args.copy_mb, dev)
     head = "fp16" if "fp16" in results else next(iter(results))
@@ -762,6 +819,7 @@ def main():
         "streamk": sk,
         "splitk": splitk,
         "moe": moe,
+        "fmha": fmha,
     }
     if args.cpu_baseline and not args.only:
         line["cpu_baseline"] = cpu_baseline(M, N, K, dev, seeds)

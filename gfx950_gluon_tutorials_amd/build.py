@@ -25,6 +25,11 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 # profiling.py; never loaded by the wrappers unless G9_LIBRARY points at it.
 LIB_TIMING_PATH = os.path.join(PKG_DIR, "libg9gemm_timing.so")
 SOURCES = ["g9_capi.hip", "g9_fmha.hip"]  # GEMM + MoE + C ABI; flash-attention forward
+# Per-source flags.  g9_fmha.hip: without NaN-preserving semantics for fmax
+# the row-max reduction is one v_max3 per two scores instead of also
+# canonicalizing every MFMA result first (NaN inputs still give NaN rows:
+# their exponentials are NaN).
+SOURCE_FLAGS = {"g9_fmha.hip": ["-fno-honor-nans"]}
 HEADERS = ["g9_common.hpp", "g9_gemm.hpp"]
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_*_f32, whose results
@@ -71,7 +76,7 @@ def build(verbose: bool = False, timing: bool = False) -> str:
             d = os.path.join(work, os.path.splitext(src)[0])
             os.makedirs(d)
             obj = os.path.join(d, src + ".o")
-            cmd = [hipcc_path(), *[f for f in flags if f != "-shared"], "-c", "-save-temps", "-I",
+            cmd = [hipcc_path(), *[f for f in flags if f != "-shared"], *SOURCE_FLAGS.get(src, []), "-c", "-save-temps", "-I",
                    os.path.join(REPO_DIR, "include"), os.path.join(CSRC, src), "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)

@@ -23,11 +23,8 @@
 // element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12
 // (measured on gfx950): 4 keys of one head-dim column per read.
 //
-// K and V tiles (64 rows x 256 bytes) are double buffered in LDS and filled by
-// LDS-DMA.  The 16-byte chunk c of row r sits at chunk slot c ^ swz(r & 15),
-// which keeps the 16-row K reads and the 4-row V transpose reads free of bank
-// conflicts; the DMA applies it on the global side (each lane fetches the
-// chunk that belongs in its LDS slot).
+// The loop is software pipelined over four clusters with the two waves of a
+// SIMD one cluster apart (see Pipe below).
 #include <stdint.h>
 
 #include "../../include/gfx950_fmha.h"
@@ -36,11 +33,33 @@
 namespace g9 {
 namespace fa {
 
+// Optional phase stamps (build with -DG9_TIMING; read by profiling.py through
+// g9_fmha_timing_read): thread 0 of each workgroup records s_memtime (shader
+// clock) and s_memrealtime (100 MHz) at kernel entry, loop start, loop end and
+// kernel end, for the first kTimingWorkgroups workgroups (by block index).
+// Each stamp waits only for its own scalar reads.  Nothing in the regular
+// build.
+#ifdef G9_TIMING
+constexpr int kTimingWorkgroups = 16384;
+__device__ unsigned long long g9_fmha_timing_buf[kTimingWorkgroups * 8];
+G9_DEV void stamp(int slot) {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memtime();
+  const unsigned long long r = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));  // lgkmcnt(0) only
+  if (threadIdx.x == 0 && blockIdx.x < kTimingWorkgroups) {
+    g9_fmha_timing_buf[blockIdx.x * 8 + slot * 2] = t;
+    g9_fmha_timing_buf[blockIdx.x * 8 + slot * 2 + 1] = r;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+#else
+G9_DEV void stamp(int) {}
+#endif
+
 constexpr int kBlockM = 256;                // query rows per workgroup
 constexpr int kBlockN = 64;                 // keys per tile
 constexpr int kHd = 128;                    // head dim
-constexpr int kRowBytes = kHd * 2;          // one K/V row (256 bytes)
-constexpr int kTileBytes = kBlockN * kRowBytes;  // one K or V tile (16 KiB)
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -64,12 +83,6 @@ struct FaParams {
   float scale_log2;                  // sm_scale * log2(e)
   int scale_on_q;                    // fold scale_log2 into Q (rounded to 16 bit) before the loop
 };
-
-// Chunk swizzle of row r (a bijection of 0..15): 16 consecutive rows get 16
-// distinct values, and 4 consecutive rows from a multiple of 4 get distinct
-// bits 1-2, so the K reads (16 rows, one chunk) and the V transpose reads (4
-// rows, one 32-byte chunk pair) both cover distinct banks.
-G9_DEV int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8); }
 
 // MFMA 32x32x16 on 16-bit operands given as raw registers.
 template <bool BF16>
@@ -102,18 +115,6 @@ G9_DEV f32x2 unpack2(u32 w) {
   } else {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     return __builtin_convertvector(__builtin_bit_cast(h2, w), f32x2);
-  }
-}
-
-// acc + the two 16-bit values of w (fp32 accumulate).
-template <bool BF16>
-G9_DEV float dot2_ones(u32 w, float acc) {
-  if constexpr (BF16) {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, w), __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
-  } else {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), __builtin_bit_cast(h2, 0x3c003c00u), acc, false);
   }
 }
 
@@ -156,194 +157,17 @@ G9_DEV u32x2 tr_read(u32 addr) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-template <bool BF16, bool LAZY>
-G9_DEV void fmha_fwd(const FaParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // K0 K1 V0 V1
-  // Workgroups of one (batch, head) run consecutively on one XCD, so its L2
-  // serves their shared K and V.
-  const int total = p.B * p.HQ * p.mblocks;
-  int pid, unused;
-  tile_coords(blockIdx.x, total, total, 1, p.num_xcds, 1, pid, unused);
-  const int bh = pid / p.mblocks, mb = pid - bh * p.mblocks;
-  const int b = bh / p.HQ, hq = bh - b * p.HQ;
-  const int hk = hq * p.HK / p.HQ;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = lane >> 5;  // lane half
-  const int nt = p.S / kBlockN;
-  const u32 lds0 = (u32)(uintptr_t)to_lds(smem);
-
-  const char* qb = p.q + b * p.q_b + hq * p.q_h;
-  const char* kb = p.k + b * p.k_b + hk * p.k_h;
-  const char* vb = p.v + b * p.v_b + hk * p.v_h;
-  const rsrc_t rq = make_rsrc(qb, (u32)p.S * p.ldq);
-  const rsrc_t rk = make_rsrc(kb, (u32)p.S * p.ldk);
-  const rsrc_t rv = make_rsrc(vb, (u32)p.S * p.ldv);
-
-  // Q fragments (B operand of S^T = K Q^T): lane l holds Q[q][16s + 8h .. + 7]
-  // of query q = row0 + l % 32, for s = 0..7.  Rows past S read zero.
-  const int qrow = mb * kBlockM + wave * 32 + (lane & 31);
-  u32x4 qf[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (u32)qrow * p.ldq + (16 * s + 8 * h) * 2, 0, 0));
-  // With scale_on_q the scores come out of the MFMA already in log2 units.
-  float sc = p.scale_log2;
-  if (p.scale_on_q) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f32x2 x = unpack2<BF16>(qf[s][e]);
-        qf[s][e] = pack2<BF16>(x.x * sc, x.y * sc);
-      }
-    sc = 1.f;
-  }
-
-  // DMA of one K or V tile: wave w fills rows 8w..8w+7 with two 16-byte DMAs
-  // of 4 rows each; lane i fetches the chunk that belongs in LDS slot i.
-  u32 voffk[2], voffv[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = 8 * wave + 4 * t + (lane >> 4);
-    const int ch = (lane & 15) ^ swz(row & 15);
-    voffk[t] = (u32)row * p.ldk + ch * 16;
-    voffv[t] = (u32)row * p.ldv + ch * 16;
-  }
-  auto issue = [&](int tile, int buf) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const u32 dst = lds0 + buf * kTileBytes + (8 * wave + 4 * t) * kRowBytes;
-      dma16(rk, (G9_LDS void*)(uintptr_t)dst, voffk[t], (u32)tile * kBlockN * p.ldk);
-      dma16(rv, (G9_LDS void*)(uintptr_t)(dst + 2 * kTileBytes), voffv[t], (u32)tile * kBlockN * p.ldv);
-    }
-  };
-  issue(0, 0);
-  if (nt > 1) issue(1, 1);
-
-  // LDS read addresses (relative to the buffer).  K: lane l reads row l % 32
-  // (+32 per block), chunk 2s + h.  V: lane 16G + j reads row 4(G/2) + j/4
-  // (+8 for the second read, +16 per step), 8 bytes at head-dim column
-  // 32 dblk + 16(G % 2) + 4(j % 4).
-  u32 ak[8], av[4][2];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) ak[s] = (u32)(lane & 31) * kRowBytes + (((2 * s + h) ^ swz(lane & 15)) << 4);
-  {
-    const int G = lane >> 4, j = lane & 15;
-#pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-      for (int sec = 0; sec < 2; ++sec) {
-        const int row = 4 * (G >> 1) + (j >> 2) + 8 * sec;
-        const int ch = 4 * dblk + 2 * (G & 1) + ((j & 3) >> 1);
-        av[dblk][sec] = (u32)row * kRowBytes + ((ch ^ swz(row & 15)) << 4) + 8 * (j & 1);
-      }
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
-  float m = -__builtin_inff(), l = 0.f;
-
-  for (int j = 0; j < nt; ++j) {
-    const u32 kbuf = lds0 + (j & 1) * kTileBytes;
-    const u32 vbuf = kbuf + 2 * kTileBytes;
-    // Tile j's DMAs (all waves') landed; tile j + 1's may still be in flight.
-    if (j + 1 < nt)
-      waitcnt<4, 15>();
-    else
-      waitcnt<0, 15>();
-    barrier();
-
-    f32x16 s0 = {}, s1 = {};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 k0 = *(const G9_LDS u32x4*)(uintptr_t)(kbuf + ak[s]);
-      const u32x4 k1 = *(const G9_LDS u32x4*)(uintptr_t)(kbuf + ak[s] + 32 * kRowBytes);
-      s0 = mfma<BF16>(k0, qf[s], s0);
-      s1 = mfma<BF16>(k1, qf[s], s1);
-    }
-
-    // Online softmax in log2 units: x = s * sm_scale * log2(e).  LAZY keeps
-    // the running max unless the tile's max exceeds it by more than
-    // kLazyThreshold (p then stays below 2^kLazyThreshold; o and l share the
-    // stale frame, so o / l is unchanged) and skips the rescale of o when no
-    // row of the wave moved.
-    float mx = s0[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, s0[i]);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, s1[i]);
-    mx = xhalf(mx, [](float a, float c) { return __builtin_fmaxf(a, c); });
-    const float mt = mx * sc;
-    const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    float rs = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], sc, -m_new));
-      s1[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], sc, -m_new));
-      rs += s0[i] + s1[i];
-    }
-    l = l * alpha + rs;
-    m = m_new;
-    if (!LAZY || __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] *= alpha;
-    }
-
-    // P^T fragments: step t, slot u = score register 8(t % 2) + u of block t / 2.
-    u32x4 pf[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f32x16& sv = t < 2 ? s0 : s1;
-      const int r0 = 8 * (t & 1);
-      pf[t] = u32x4{pack2<BF16>(sv[r0 + 0], sv[r0 + 1]), pack2<BF16>(sv[r0 + 2], sv[r0 + 3]),
-                    pack2<BF16>(sv[r0 + 4], sv[r0 + 5]), pack2<BF16>(sv[r0 + 6], sv[r0 + 7])};
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const u32x2 lo = tr_read(vbuf + av[d][0] + t * 16 * kRowBytes);
-        const u32x2 hi = tr_read(vbuf + av[d][1] + t * 16 * kRowBytes);
-        o[d] = mfma<BF16>(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[t], o[d]);
-      }
-
-    // Every wave done with this buffer before it is refilled with tile j + 2.
-    waitcnt<63, 0>();
-    barrier();
-    if (j + 2 < nt) issue(j + 2, j & 1);
-  }
-
-  // Normalise, store O (lane l: query row0 + l % 32, head-dim columns
-  // 32 dblk + 8r + 4h .. + 3 of register quad r) and the log-sum-exp.
-  const float lt = xhalf(l, [](float a, float c) { return a + c; });
-  const float inv = 1.f / lt;
-  if (qrow < p.S) {
-    char* orow = p.o + b * p.o_b + hq * p.o_h + (size_t)qrow * p.ldo;
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int col = 32 * d + 8 * r + 4 * h;
-        const u32x2 w = {pack2<BF16>(o[d][4 * r] * inv, o[d][4 * r + 1] * inv),
-                         pack2<BF16>(o[d][4 * r + 2] * inv, o[d][4 * r + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + col * 2) = w;
-      }
-    if (p.lse && h == 0) p.lse[((size_t)b * p.HQ + hq) * p.S + qrow] = (m + __builtin_log2f(lt)) * kLn2;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Pipelined form.  Each wave's loop over key tiles j is cut into four
 // clusters, each closed by a workgroup barrier:
 //   D1(j)  QK MFMAs of tile j+1 (K_{j+1} from registers) and, in their issue
 //          shadow, the second half of tile j's softmax (the remaining
 //          exponentials, P_j to 16 bit, the row sum);
-//   M1(j)  LDS reads of V_j; DMA of K_{j+3};
-//   D2(j)  PV MFMAs of tile j and, in their shadow, the first half of tile
-//          j+1's softmax (row max, new running max, most exponentials);
+//   M1(j)  LDS reads of V_j; DMA of K_{j+3}; tile j+1's row max, new running
+//          max and rescale factor (a dependent chain: it would stall MFMA
+//          issue in a dot cluster, here it fills the idle VALU);
+//   D2(j)  PV MFMAs of tile j and, in their shadow, most of tile j+1's
+//          exponentials;
 //   M2(j)  LDS reads of K_{j+2}; DMA of V_{j+2}; rescale of O and l.
 // Waves 4-7 run one cluster behind waves 0-3, so on every SIMD one wave is in
 // a dot cluster (MFMA + VALU) while the other is in a memory cluster: the
@@ -369,7 +193,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
 #define G9_FMHA_VN2 4  // VALU instructions after each PV MFMA of D2
 #endif
 #ifndef G9_FMHA_VEC1_EXPS
-#define G9_FMHA_VEC1_EXPS 20  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
+#define G9_FMHA_VEC1_EXPS 18  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
 #endif
 
 constexpr int kPitchK = 1024;                  // bytes between K chunk columns
@@ -459,9 +283,10 @@ struct Pipe {
       s1[i - 16] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i - 16], sc, -m));
   }
 
-  // First half of a tile's softmax: row max, running max, alpha, and the
-  // first kE1 exponentials (in place).
-  G9_DEV void vec1(f32x16& s0, f32x16& s1) {
+  // Start of a tile's softmax: row max, running max and alpha (a dependent
+  // chain ending in a cross-lane exchange; run in a memory cluster, where the
+  // VALU is otherwise idle, so the MFMA shadows keep only independent work).
+  G9_DEV void vec0(f32x16& s0, f32x16& s1) {
     float a = __builtin_fmaxf(__builtin_fmaxf(s0[0], s0[1]), s0[2]);
     float b = __builtin_fmaxf(__builtin_fmaxf(s0[8], s0[9]), s0[10]);
     float c = __builtin_fmaxf(__builtin_fmaxf(s1[0], s1[1]), s1[2]);
@@ -480,17 +305,31 @@ struct Pipe {
     const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
     alpha = __builtin_amdgcn_exp2f(m - m_new);
     m = m_new;
+  }
+  // First kE1 exponentials of a tile (in place).
+  G9_DEV void vec1(f32x16& s0, f32x16& s1) {
 #pragma unroll
     for (int i = 0; i < kE1; ++i) expo(s0, s1, i);
   }
-  // Second half: the remaining exponentials, P to 16 bit, l += row sum (of
-  // the rounded values, which is what the PV MFMAs weight V with).  The
-  // 16-bit pairs of PV step t are written over the first four registers of
-  // their eight scores (registers 8(t % 2) .. +3 of block t / 2), so P needs
-  // no registers of its own.
+  // Second half: the remaining exponentials, l += row sum (fp32, before
+  // rounding), P to 16 bit.  The 16-bit pairs of PV step t are written over
+  // the first four registers of their eight scores (registers 8(t % 2) .. +3
+  // of block t / 2), so P needs no registers of its own.  (The row sum uses
+  // plain adds: v_dot2c on the packed values would take half the
+  // instructions but does not issue beside an MFMA -- measured: two per MFMA
+  // stretch its 32-cycle interval to 53.)
   G9_DEV void vec2(f32x16& s0, f32x16& s1) {
 #pragma unroll
     for (int i = kE1; i < 32; ++i) expo(s0, s1, i);
+    float r0 = s0[0] + s0[1], r1 = s0[8] + s0[9], r2 = s1[0] + s1[1], r3 = s1[8] + s1[9];
+#pragma unroll
+    for (int i = 2; i < 8; ++i) {
+      r0 += s0[i];
+      r1 += s0[8 + i];
+      r2 += s1[i];
+      r3 += s1[8 + i];
+    }
+    l += (r0 + r1) + (r2 + r3);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f32x16& sv = t < 2 ? s0 : s1;
@@ -498,10 +337,6 @@ struct Pipe {
 #pragma unroll
       for (int e = 0; e < 4; ++e) sv[r0 + e] = __uint_as_float(pack2<BF16>(sv[r0 + 2 * e], sv[r0 + 2 * e + 1]));
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) l = dot2_ones<BF16>(__float_as_uint((t < 2 ? s0 : s1)[8 * (t & 1) + e]), l);
   }
   // Pins the 16-bit P pairs and l (vec2's results).
   G9_DEV void pin_p(f32x16& s0, f32x16& s1) {
@@ -522,15 +357,16 @@ struct Pipe {
   }
 
   // Interleave of a dot cluster: MFMA i followed by VN VALU instructions.
+  // An MFMA 32x32x16 takes 32 cycles; about six plain VALU instructions or
+  // two to three exponentials issue beside it without delaying the next one
+  // (measured).
   template <int VN>
   G9_DEV static void interleave() {
-#ifndef G9_FMHA_NO_INTERLEAVE
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
       __builtin_amdgcn_sched_group_barrier(SG_VALU, VN, 0);
     }
-#endif
   }
 
   // One loop iteration; PAR = j & 1 fixes the LDS buffers; (c0, c1) hold
@@ -565,6 +401,9 @@ struct Pipe {
         n0 = f32x16{} - __builtin_inff();
         n1 = n0;
       }
+      vec0(n0, n1);
+      pin(m);
+      pin(alpha);
     }
     waitcnt<63, 0>();
     barrier();
@@ -575,8 +414,6 @@ struct Pipe {
       interleave<G9_FMHA_VN2>();
       pin_vec(n0);
       pin_vec(n1);
-      pin(m);
-      pin(alpha);
     } else {
       pv(c0, c1);
     }
@@ -599,8 +436,9 @@ struct Pipe {
 };
 
 template <bool BF16, bool LAZY>
-G9_DEV void fmha_fwd_pp(const FaParams& p) {
+G9_DEV void fmha_fwd(const FaParams& p) {
   __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  stamp(0);
   const int total = p.B * p.HQ * p.mblocks;
   int pid, unused;
   tile_coords(blockIdx.x, total, total, 1, p.num_xcds, 1, pid, unused);
@@ -662,12 +500,14 @@ G9_DEV void fmha_fwd_pp(const FaParams& p) {
   barrier();  // every wave has read K_0: its buffer takes K_2
   if (nte > 2) P.dma_k(2, 0);
   P.dma_v(1, 1);
+  P.vec0(sa0, sa1);
   P.vec1(sa0, sa1);
   P.l *= P.alpha;
   P.template read_k<1>();
   waitcnt<63, 0>();
 
   const bool lag = wave >= 4;
+  stamp(1);
   if (lag) barrier();
   int j = 0;
   for (; j + 2 < nte; j += 2) {
@@ -677,6 +517,7 @@ G9_DEV void fmha_fwd_pp(const FaParams& p) {
   P.template step<0, true>(j, sa0, sa1, sb0, sb1);
   P.template step<1, false>(j + 1, sb0, sb1, sa0, sa1);
   if (!lag) barrier();
+  stamp(2);
 
   const float lt = xhalf(P.l, [](float x, float y) { return x + y; });
   const float inv = 1.f / lt;
@@ -693,6 +534,7 @@ G9_DEV void fmha_fwd_pp(const FaParams& p) {
       }
     if (p.lse && h == 0) p.lse[((size_t)b * p.HQ + hq) * p.S + qrow] = (P.m + __builtin_log2f(lt)) * kLn2;
   }
+  stamp(3);
 }
 
 }  // namespace fa
@@ -700,16 +542,11 @@ G9_DEV void fmha_fwd_pp(const FaParams& p) {
 
 using namespace g9;
 
-#ifndef G9_FMHA_SIMPLE
-#define FMHA_IMPL fmha_fwd_pp
-#else
-#define FMHA_IMPL fmha_fwd
-#endif
 // Kernels: g9_fmha_fwd_{bf16,f16}_v{3,4}; v3 rescales every tile, v4 lazily.
 #define G9_FMHA_KERNEL(NAME, BF16, LAZY)                                                                   \
   extern "C" __global__ __launch_bounds__(fa::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void \
   NAME(fa::FaParams p) {                                                                                  \
-    fa::FMHA_IMPL<BF16, LAZY>(p);                                                                        \
+    fa::fmha_fwd<BF16, LAZY>(p);                                                                           \
   }
 G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false)
 G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false)
@@ -776,3 +613,14 @@ extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o,
              ? G9_OK
              : G9_ERR_HIP;
 }
+
+#ifdef G9_TIMING
+#include "../../include/gfx950_gemm_timing.h"
+extern "C" int g9_fmha_timing_read(void* host, size_t bytes) {
+  if (bytes > sizeof(g9::fa::g9_fmha_timing_buf)) return G9_ERR_SHAPE;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g9::fa::g9_fmha_timing_buf), bytes, 0, hipMemcpyDeviceToHost) ==
+                 hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}
+#endif

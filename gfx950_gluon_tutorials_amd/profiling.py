@@ -182,6 +182,58 @@ def measure(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.
     return out
 
 
+def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s: float = 0.8) -> dict:
+    """Phase statistics of one flash-attention launch (g9_fmha_fwd, bhsd,
+    head dim 128) at steady state, as ``measure``.  The loop covers all key
+    tiles of 64 (an even count); each costs 2048 ideal MFMA cycles per SIMD
+    (2 waves x 32 MFMAs 32x32x16 x 32 cycles), so phase_stats applies with
+    stages = tiles."""
+    import ctypes
+    import time
+
+    import torch
+
+    from . import _lib
+    from .attention import MetaData, compute_flops, fmha_v3, fmha_v4
+
+    lib = _lib.load()
+    if not hasattr(lib, "g9_fmha_timing_read"):
+        raise RuntimeError(f"{_lib.LIB_PATH} is not the timing build (python -m gfx950_gluon_tutorials_amd.build --timing)")
+    lib.g9_fmha_timing_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    dev = torch.device("cuda:0")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    g = torch.Generator().manual_seed(0)
+    q, k, v = ((torch.randn(B, H, S, 128, generator=g)).to(tdt).to(dev) for _ in range(3))
+    o = torch.empty_like(q)
+    md = MetaData(sm_scale=128**-0.5)
+    md.max_seqlens_q = md.max_seqlens_k = S
+    md.layout = "bhsd"
+    fn = fmha_v4.run_gluon_attention if variant == 4 else fmha_v3.run_gluon_attention
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        for _ in range(5):
+            fn(q, k, v, o, md)
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        fn(q, k, v, o, md)
+    e1.record()
+    torch.cuda.synchronize()
+    launch_us = e0.elapsed_time(e1) / 20 * 1e3
+    fn(q, k, v, o, md)
+    torch.cuda.synchronize()
+    wgs = B * H * -(-S // 256)
+    n = min(wgs, lib.g9_timing_capacity())
+    buf = np.zeros(n * 8, dtype=np.uint64)
+    _lib.check(lib.g9_fmha_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_fmha_timing_read")
+    tiles = (S // 64 + 1) // 2 * 2
+    out = phase_stats(buf, tiles)
+    out.update({"kernel": f"fmha_v{variant}", "dtype": dtype, "B": B, "H": H, "S": S, "launch_us": round(launch_us, 2),
+                "tflops": round(compute_flops(B, H, S, S, 128, False) / launch_us / 1e6, 1)})
+    return out
+
+
 def sk_stats(stamps: np.ndarray, M: int, N: int, stage_k: int, K: int) -> dict:
     """Summarises stream-K stamps (persistent workgroups x 8 uint64: clock and
     100 MHz clock at entry and exit, flag-wait / partial-load / partial-store
@@ -350,10 +402,28 @@ def main(argv=None) -> int:
     ap.add_argument("--json", help="also write the results to this file")
     ap.add_argument("--streamk", action="store_true",
                     help="stream-K fixup cost instead (give --M/--N/--K; e.g. 8192 1280 8192)")
+    ap.add_argument("--fmha", help="flash-attention forward instead: B,H,S (e.g. 32,8,8192); "
+                    "--dtypes fp16/bf16, --waves is ignored")
+    ap.add_argument("--variants", default="4", help="with --fmha: 3, 4 or 3,4")
     ap.add_argument("--operands", help="FP16 launch time per operand distribution instead "
                     f"(comma-separated from {','.join(OPERAND_KINDS)})")
     args = ap.parse_args(argv)
     results = []
+    if args.fmha:
+        B, H, S = (int(x) for x in args.fmha.split(","))
+        for dt in args.dtypes.split(","):
+            for var in (int(x) for x in args.variants.split(",")):
+                r = measure_fmha(dt, B, H, S, var)
+                results.append(r)
+                print(f"fmha_v{var} {dt} B={B} H={H} S={S} D=128: {r['launch_us']:.1f} us/launch "
+                      f"({r['tflops']:.0f} TFLOPS)  loop MFMA eff {r['mfma_efficiency']:.3f}  clock "
+                      f"{r['clock_ghz']:.3f} GHz  prologue {r['prologue_cycles']}  loop {r['loop_cycles']} (ideal "
+                      f"{r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles | workgroup "
+                      f"{r['workgroup_us']:.1f} us, span {r['span_us']:.1f} us", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(results, f, indent=1)
+        return 0
     if args.operands:
         for w in (int(v) for v in args.waves.split(",")):
             for r in operand_study(args.operands.split(","), args.M, args.N, int(args.K.split(",")[0]), w):

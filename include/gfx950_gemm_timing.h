@@ -26,6 +26,11 @@ int g9_timing_read(void* host, size_t bytes);
 /* Number of workgroups the buffer holds stamps for. */
 int g9_timing_capacity(void);
 
+/* Same for the flash-attention kernel (its own buffer, the same capacity):
+ * (shader clock, 100 MHz clock) at kernel entry, loop start, loop end and
+ * kernel end per workgroup, as left by the last g9_fmha_fwd launch. */
+int g9_fmha_timing_read(void* host, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -176,3 +176,25 @@ def test_benchmark_shape_on_sampled_rows(gpu, dtype):
         assert ok, f"row {(b, h, s)}: max |diff| {mx:.3g}"
         bound = np.abs(qq[s]).sum() * np.abs(kk).max() * md.sm_scale
         assert abs(got_l[b, h, s] - ref_l[0]) <= 2 * A.FINFO_EPS[DT_NAME[DT[dtype]]] * bound + 1e-4
+
+
+@pytest.mark.parametrize("variant", [3, 4])
+def test_nan_inputs_give_nan_rows(gpu, variant):
+    # As the reference's fp32 SDPA: a NaN in a query row makes that row NaN; a
+    # NaN in a key row makes every row of the heads reading that K head NaN.
+    # Everything else is unaffected.
+    q, k, v, md = _inputs(1, 4, 2, 256, torch.bfloat16, "bhsd", seed=13)
+    q[0, 1, 5, 3] = float("nan")
+    k[0, 1, 100, 7] = float("nan")  # K head 1 = query heads 2, 3
+    o, _ = _run(q, k, v, md, gpu, variant, lse=False)
+    o = o.float()
+    assert torch.isnan(o[0, 1, 5]).all()
+    assert torch.isnan(o[0, 2:]).all()
+    keep = torch.ones(4, 256, dtype=torch.bool)
+    keep[1, 5] = False
+    keep[2:] = False
+    got = o[0][keep]
+    assert torch.isfinite(got).all()
+    ref, _ = A.sdpa_reference(q.float().numpy(), k.float().numpy(), v.float().numpy(), md.sm_scale)
+    ok, mx, _ = A.within_tolerance(got.numpy(), ref[0][keep.numpy()], "bfloat16")
+    assert ok, mx

@@ -36,7 +36,7 @@ def test_timing_build_exports_its_header_and_the_regular_one_does_not():
 
     text = open(TIMING_HEADER).read()
     names = sorted(set(re.findall(r"^\s*\w+\s*\*?\s*(g9_\w+)\s*\(", text, flags=re.M)))
-    assert names == ["g9_timing_capacity", "g9_timing_read"]
+    assert names == ["g9_fmha_timing_read", "g9_timing_capacity", "g9_timing_read"]
     regular = _lib.load()
     for n in names:
         assert not hasattr(regular, n), f"{n} leaked into the regular library"
