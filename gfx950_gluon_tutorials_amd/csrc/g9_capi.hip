@@ -262,7 +262,7 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
-                 const void* c);
+                 const void* c, bool allow_tail = false);
 
 // Shared launch path of the grouped kernels: T token rows, E experts.
 int launch_moe(int dtype, int out, GemmParams& p, int64_t E, void* stream) {
@@ -297,21 +297,27 @@ int check_moe(int64_t T, int64_t N, int64_t K, int64_t E, int dtype, int64_t str
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
-                 const void* c) {
+                 const void* c, bool allow_tail) {
   if (M <= 0 || N <= 0 || K <= 0) return G9_ERR_SHAPE;
   if (M > (1 << 30) || N > (1 << 30)) return G9_ERR_SHAPE;
   // Tile ids and the data-parallel grid are 32-bit.
   if (((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile) > INT32_MAX) return G9_ERR_SHAPE;
   const int sk = stage_k(dtype);
-  if (K % sk != 0 || K / sk >= 65536) return G9_ERR_SHAPE;
+  // K tails (FP16/BF16/BF8 dense GEMMs): a partial first stage, whole 16-byte
+  // chunks (K a multiple of 8 for 16-bit types, 16 for BF8).
+  const int64_t chunk_k = sk / 8;  // elements per 16 bytes: 8 (16-bit), 16 (8-bit)
+  if (allow_tail ? K % chunk_k != 0 : K % sk != 0) return G9_ERR_SHAPE;
+  if ((K + sk - 1) / sk >= 65536) return G9_ERR_SHAPE;
   if (stride_cn != 1 || stride_cm < N || !aligned(c, 2)) return G9_ERR_LAYOUT;
   return G9_OK;
 }
 
-int check_operand(const void* p, int64_t row_stride_bytes, int64_t k_stride, int64_t k_bytes) {
+int check_operand(const void* p, int64_t row_stride_bytes, int64_t k_stride, int64_t k_bytes, bool k_tail = false) {
   if (k_stride != 1) return G9_ERR_LAYOUT;
   if (!aligned(p, 16) || row_stride_bytes % 16 != 0 || row_stride_bytes < k_bytes) return G9_ERR_LAYOUT;
-  if (row_stride_bytes > (1 << 24)) return G9_ERR_LAYOUT;  // 128 rows x stride must fit 32-bit offsets
+  // 128 rows x stride must fit 31-bit offsets (dead offsets start at 2^31);
+  // a K tail adds up to 112 bytes to a resource, so the stride stays below 2^24.
+  if (row_stride_bytes > (1 << 24) || (k_tail && row_stride_bytes >= (1 << 24))) return G9_ERR_LAYOUT;
   return G9_OK;
 }
 
@@ -323,10 +329,10 @@ int prep_a16w16(GemmParams& p, const void* a, const void* b, void* c, int64_t M,
                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn, int64_t stride_cm,
                 int64_t stride_cn, int dtype) {
   if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
-  int st = check_common(M, N, K, dtype, stride_cm, stride_cn, c);
+  int st = check_common(M, N, K, dtype, stride_cm, stride_cn, c, /*allow_tail=*/true);
   if (st) return st;
-  if ((st = check_operand(a, stride_am * 2, stride_ak, K * 2))) return st;
-  if ((st = check_operand(b, stride_bn * 2, stride_bk, K * 2))) return st;
+  if ((st = check_operand(a, stride_am * 2, stride_ak, K * 2, K % 64 != 0))) return st;
+  if ((st = check_operand(b, stride_bn * 2, stride_bk, K * 2, K % 64 != 0))) return st;
   p = GemmParams{};
   p.a = static_cast<const char*>(a);
   p.b = static_cast<const char*>(b);
@@ -337,7 +343,8 @@ int prep_a16w16(GemmParams& p, const void* a, const void* b, void* c, int64_t M,
   p.lda = (u32)(stride_am * 2);
   p.ldb = (u32)(stride_bn * 2);
   p.ldc = stride_cm;
-  p.ns = (int)(K / stage_k(dtype));
+  p.ns = (int)((K + 63) / 64);
+  p.kshift = (u32)(p.ns * 128 - K * 2);
   return G9_OK;
 }
 }  // namespace
@@ -361,10 +368,10 @@ int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, in
                  int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
                  void* stream) {
   if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
-  int st = check_common(M, N, K, G9_BF8, stride_cm, stride_cn, c);
+  int st = check_common(M, N, K, G9_BF8, stride_cm, stride_cn, c, /*allow_tail=*/true);
   if (st) return st;
-  if ((st = check_operand(a, stride_am, stride_ak, K))) return st;
-  if ((st = check_operand(b, stride_bn, stride_bk, K))) return st;
+  if ((st = check_operand(a, stride_am, stride_ak, K, K % 128 != 0))) return st;
+  if ((st = check_operand(b, stride_bn, stride_bk, K, K % 128 != 0))) return st;
   if ((a_scale && !aligned(a_scale, 4)) || (b_scale && !aligned(b_scale, 4))) return G9_ERR_LAYOUT;
   GemmParams p{};
   p.a = static_cast<const char*>(a);
@@ -378,7 +385,8 @@ int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, in
   p.lda = (u32)stride_am;
   p.ldb = (u32)stride_bn;
   p.ldc = stride_cm;
-  p.ns = (int)(K / stage_k(G9_BF8));
+  p.ns = (int)((K + 127) / 128);
+  p.kshift = (u32)(p.ns * 128 - K);
   return launch(G9_BF8, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
 }
 
@@ -553,7 +561,7 @@ size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedul
   const long long tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
   if (schedule == G9_SCHED_SPLITK) {
     const int cus = cu_count();
-    const int S = cus > 0 ? g9_splitk_factor(tiles, (int)(K / stage_k(dtype)), cus) : 1;
+    const int S = cus > 0 ? g9_splitk_factor(tiles, (int)((K + stage_k(dtype) - 1) / stage_k(dtype)), cus) : 1;
     return S > 1 ? splitk_bytes(tiles * S) : 0;
   }
   if (schedule != G9_SCHED_SK) return 0;

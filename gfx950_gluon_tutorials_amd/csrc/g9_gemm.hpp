@@ -131,7 +131,9 @@ struct GemmParams {
   u32 lda, ldb;               // operand row strides in bytes
   u32 ldsa, ldsb;             // scale row strides in bytes
   long long ldc;              // C row stride in elements
-  int ns;                     // K stages (K * bits / 1024)
+  int ns;                     // K stages (ceil(K * bits / 1024))
+  u32 kshift;                 // K tail: bytes by which stage 0 starts before k = 0 (ns * 128 - K bytes);
+                              // the operand resources start that much earlier, stage 0's DMAs zero it
   int tiles_m, tiles_n;
   int num_xcds, group_m;
   // stream-K
@@ -515,6 +517,7 @@ struct Pipe {
   int wave;
   int s0;                   // first stage of the range (chunks are counted from here)
   int s_end;                // first stage not to load
+  u32 kshift;               // GemmParams::kshift
 
   G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int first, int end) {
     // Tile coordinates are wave-uniform; saying so keeps the buffer resources
@@ -524,6 +527,7 @@ struct Pipe {
     tn = __builtin_amdgcn_readfirstlane(tn);
     s0 = __builtin_amdgcn_readfirstlane(first);
     s_end = __builtin_amdgcn_readfirstlane(end);
+    kshift = p.kshift;
     lds0 = (u32)(uintptr_t)to_lds(smem);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -538,8 +542,12 @@ struct Pipe {
       // resources stay in SGPRs.
       const int va = __builtin_amdgcn_readfirstlane(min(max(p.M - ra, 0), 128));
       const int vb = __builtin_amdgcn_readfirstlane(min(max(p.N - rb, 0), 128));
-      rA[h] = make_rsrc(p.a + (size_t)ra * p.lda, (u32)va * p.lda);
-      rB[h] = make_rsrc(p.b + (size_t)rb * p.ldb, (u32)vb * p.ldb);
+      // A K tail shifts every stage by kshift bytes: stage s covers row bytes
+      // [128 s - kshift, 128 (s + 1) - kshift), so the base moves back by
+      // kshift (and the valid range grows by it) while the DMA offsets stay
+      // 128 s + chunk; stage 0's chunks before k = 0 are zeroed (issue()).
+      rA[h] = make_rsrc(p.a + (size_t)ra * p.lda - p.kshift, (u32)va * p.lda + p.kshift);
+      rB[h] = make_rsrc(p.b + (size_t)rb * p.ldb - p.kshift, (u32)vb * p.ldb + p.kshift);
     }
     // DMA j of a sub-buffer covers rows 8j..8j+7 of the wave's share and is
     // issued with immediate offset 1024j, which advances the LDS destination
@@ -712,11 +720,25 @@ struct Pipe {
       sr.b1[F] = v;
   }
 
-  // Whole-set variants for the prologue.
+  // Whole-set variants for the prologue.  Stage 0 of a K tail: the lanes
+  // whose 16-byte chunk lies before k = 0 (chunk * 16 < kshift) get a dead
+  // offset, so they load zeros instead of the previous row's last bytes (or
+  // bytes before the operand).  Only the prologue ever issues stage 0.
   template <int X, int SLOT>
   G9_DEV void issue(int stage) const {
     const rsrc_t r = src(X);
     const u32 soff = stage_off(stage);
+    if (stage == 0 && kshift != 0) {
+      const int lane = threadIdx.x & 63;
+      static_for<D>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
+        const int ch = (lane & 7) ^ ((row >> 1) & 7);
+        const u32 v = (u32)ch * 16 < kshift ? kDeadOff : (X < 2 ? vA[j] : vB[j]);
+        dma16<j * 1024>(r, (G9_LDS void*)(uintptr_t)(mrow + sub_off(X, SLOT)), v, soff);
+      });
+      return;
+    }
     [&]<int... J>(std::integer_sequence<int, J...>) { (dma_rows<X, SLOT, J>(r, soff, mrow), ...); }(
         std::make_integer_sequence<int, D>{});
   }

@@ -37,7 +37,7 @@ extern "C" {
 /* Status codes. */
 enum {
   G9_OK = 0,
-  G9_ERR_SHAPE = 1,     /* non-positive or unsupported M/N/K (K must be a multiple of the K stage) */
+  G9_ERR_SHAPE = 1,     /* non-positive or unsupported M/N/K (K granularity: see each entry point) */
   G9_ERR_LAYOUT = 2,    /* K stride != 1, N stride of C != 1, operand rows not 16-byte aligned */
   G9_ERR_DTYPE = 3,     /* unsupported element / output type */
   G9_ERR_SCHEDULE = 4,  /* unknown schedule or wave count */
@@ -60,7 +60,10 @@ enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1, G9_SCHED_SPLITK = 2 };
  * Replaces the launch in kernels/gemm/intra_wave/a16w16/v9_beyond_hotloop/matmul_kernel.py:390-424
  * (4-wave, `waves` = 4) and the missing 8-wave kernel bound by
  * kernels/gemm/inter_wave/a16w16/bench.py:48 (`waves` = 8).
- * K must be a multiple of 64.
+ * K must be a multiple of 8 (16 bytes); the reference needs a multiple of
+ * 128.  When K is not a multiple of 64 the first K stage is partial: its
+ * loads of the missing leading chunks read zeros (operand row strides then
+ * below 2^24 bytes).
  */
 int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
                    int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
@@ -96,7 +99,8 @@ int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int
  * pointers are device fp32 scalars; NULL means 1.0.
  * Replaces kernels/gemm/intra_wave/a8w8/matmul_kernel.py:437-470 (4-wave) and
  * kernels/gemm/inter_wave/a8w8/matmul_kernel.py:343-388 (8-wave).
- * K must be a multiple of 128.
+ * K must be a multiple of 16 (16 bytes); a partial first stage when it is not
+ * a multiple of 128, as for a16w16.
  */
 int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
                  int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,

@@ -210,8 +210,8 @@ def test_a16w16_argument_validation(kw, code):
 
 def test_a8w8_and_a4w4_argument_validation():
     lib = _lib.load()
-    # a8w8: K must be a multiple of 128; output dtype fp16/bf16 only.
-    assert lib.g9_gemm_a8w8(FAKE, FAKE, FAKE, 256, 256, 192, 192, 1, 1, 192, 256, 1, None, None,
+    # a8w8: K must be a multiple of 16 (whole 16-byte chunks); output dtype fp16/bf16 only.
+    assert lib.g9_gemm_a8w8(FAKE, FAKE, FAKE, 256, 256, 200, 208, 1, 1, 208, 256, 1, None, None,
                             _lib.G9_F16, 0, 4, None, 0, None) == _lib.G9_ERR_SHAPE
     assert lib.g9_gemm_a8w8(FAKE, FAKE, FAKE, 256, 256, 256, 256, 1, 1, 256, 256, 1, None, None,
                             _lib.G9_BF8, 0, 4, None, 0, None) == _lib.G9_ERR_DTYPE

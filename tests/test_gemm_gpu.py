@@ -329,7 +329,7 @@ def test_reference_assertions_and_errors(gpu):
         a16w16_matmul(a.T, b.T)  # A not contiguous
     with pytest.raises(ValueError):
         a16w16_matmul(torch.zeros(256, 100, dtype=torch.float16, device=gpu),
-                      torch.zeros(256, 100, dtype=torch.float16, device=gpu).T)  # K % 64
+                      torch.zeros(256, 100, dtype=torch.float16, device=gpu).T)  # K % 8
     with pytest.raises(ValueError):
         a16w16_matmul(torch.zeros(256, 512, dtype=torch.float16), torch.zeros(256, 512, dtype=torch.float16).T)
     with pytest.raises(ValueError):
