@@ -79,6 +79,9 @@ def parse_args():
     p.add_argument("--fmha-only", type=int, default=0,
                    help="time only the flash-attention forward (--steps / --warmup / --settle-ms launches of each "
                         "case) and print its object (for profilers)")
+    p.add_argument("--energy", type=float, default=0.0,
+                   help="energy per launch instead: ours vs hipBLASLt for fp16 and bf16, this many seconds of "
+                        "back-to-back launches per side and round (two interleaved rounds), amd-smi power sampled")
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--serialized", type=int, default=0,
@@ -615,6 +618,39 @@ def fmha_bench(args, dev) -> dict:
     return out
 
 
+def energy_study(args, dev) -> dict:
+    """Energy per 4096x4096x8192 launch of our 4-wave data-parallel kernel and
+    of hipBLASLt's (torch.matmul) for fp16 and bf16, on one box: each side runs
+    back to back for args.energy seconds while amd-smi samples board power and
+    GFX clock (telemetry), in two interleaved rounds; energy = median power x
+    median launch time over the second half of each window."""
+    import statistics as st
+
+    import torch
+
+    M = N = 4096
+    K = 8192
+    out = {}
+    for dt in ("fp16", "bf16"):
+        nsets = max(2, -(-args.rotate_mb * 2**20 // set_bytes(dt, M, N, K)))
+        sides = {"ours": make_case(dt, M, N, K, 1, dev, nsets, 4), "hipblaslt": make_vendor_case(dt, M, N, K, 1, dev, nsets)}
+        runs = {k: [] for k in sides}
+        for _ in range(2):
+            for name, launch in sides.items():
+                tel = telemetry(launch, args.energy)
+                if tel:
+                    tel["energy_mj"] = round(tel["power_w"] * tel["launch_us"] * 1e-3, 2)
+                    runs[name].append(tel)
+                    print(f"# energy {dt} {name}: {tel['launch_us']:.1f} us at {tel['power_w']:.0f} W, "
+                          f"{tel['gfx_clock_mhz']} MHz -> {tel['energy_mj']:.1f} mJ per launch", flush=True)
+        out[dt] = {k: {"runs": v, "energy_mj": round(st.median(r["energy_mj"] for r in v), 2) if v else None,
+                       "launch_us": round(st.median(r["launch_us"] for r in v), 2) if v else None}
+                   for k, v in runs.items()}
+        del sides
+        torch.cuda.empty_cache()
+    return out
+
+
 def moe_set_bytes(dtype: str) -> int:
     E, T, N, K = (MOE_SHAPE[k] for k in ("E", "T", "N", "K"))
     if dtype == "fp16":
@@ -664,6 +700,9 @@ def main():
         return
     if args.fmha_only:
         print(json.dumps({"fmha": fmha_bench(args, dev)}), flush=True)
+        return
+    if args.energy:
+        print(json.dumps({"energy": energy_study(args, dev)}), flush=True)
         return
     dtypes = [d for d in args.dtypes.split(",") if d]
     if args.only:
