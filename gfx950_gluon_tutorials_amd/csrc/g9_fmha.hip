@@ -203,7 +203,10 @@ constexpr int kTileV = 16 * kPitchV;           // one V tile in LDS
 constexpr int kLdsV = 2 * kTileK;              // V buffers after the two K buffers
 constexpr int kLdsBytes = 2 * kTileK + 2 * kTileV;
 
-template <bool BF16, bool LAZY>
+// SOQ: the scale is folded into Q, so the scores already are in log2 units
+// and the exponent argument is a 2-source subtract instead of a 3-source fma
+// (fewer register-file reads beside the other wave's LDS returns).
+template <bool BF16, bool LAZY, bool SOQ>
 struct Pipe {
   static constexpr int kE1 = G9_FMHA_VEC1_EXPS;
   const FaParams& p;
@@ -278,9 +281,9 @@ struct Pipe {
   // register i % 16.
   G9_DEV void expo(f32x16& s0, f32x16& s1, int i) const {
     if (i < 16)
-      s0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], sc, -m));
+      s0[i] = __builtin_amdgcn_exp2f(SOQ ? s0[i] - m : __builtin_fmaf(s0[i], sc, -m));
     else
-      s1[i - 16] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i - 16], sc, -m));
+      s1[i - 16] = __builtin_amdgcn_exp2f(SOQ ? s1[i - 16] - m : __builtin_fmaf(s1[i - 16], sc, -m));
   }
 
   // Start of a tile's softmax: row max, running max and alpha (a dependent
@@ -301,7 +304,7 @@ struct Pipe {
     }
     float mx = __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
     mx = xhalf(mx, [](float x, float y) { return __builtin_fmaxf(x, y); });
-    const float mt = mx * sc;
+    const float mt = SOQ ? mx : mx * sc;
     const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
     alpha = __builtin_amdgcn_exp2f(m - m_new);
     m = m_new;
@@ -435,7 +438,7 @@ struct Pipe {
   }
 };
 
-template <bool BF16, bool LAZY>
+template <bool BF16, bool LAZY, bool SOQ>
 G9_DEV void fmha_fwd(const FaParams& p) {
   __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
   stamp(0);
@@ -448,7 +451,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int h = lane >> 5;
 
-  Pipe<BF16, LAZY> P(p);
+  Pipe<BF16, LAZY, SOQ> P(p);
   P.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   P.nt = p.S / kBlockN;
   P.nte = (P.nt + 1) & ~1;
@@ -477,7 +480,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   P.dma_v(0, 0);
   P.dma_k(1, 1);
   P.sc = p.scale_log2;
-  if (p.scale_on_q) {
+  if constexpr (SOQ) {
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
@@ -546,7 +549,10 @@ using namespace g9;
 #define G9_FMHA_KERNEL(NAME, BF16, LAZY)                                                                   \
   extern "C" __global__ __launch_bounds__(fa::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void \
   NAME(fa::FaParams p) {                                                                                  \
-    fa::fmha_fwd<BF16, LAZY>(p);                                                                           \
+    if (p.scale_on_q)                                                                                     \
+      fa::fmha_fwd<BF16, LAZY, true>(p);                                                                  \
+    else                                                                                                  \
+      fa::fmha_fwd<BF16, LAZY, false>(p);                                                                           \
   }
 G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false)
 G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false)
