@@ -193,7 +193,7 @@ G9_DEV u32x2 tr_read(u32 addr) {
 #define G9_FMHA_VN2 4  // VALU instructions after each PV MFMA of D2
 #endif
 #ifndef G9_FMHA_VEC1_EXPS
-#define G9_FMHA_VEC1_EXPS 18  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
+#define G9_FMHA_VEC1_EXPS 22  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
 #endif
 
 constexpr int kPitchK = 1024;                  // bytes between K chunk columns
