@@ -11,7 +11,7 @@ from .. import _lib
 from .common import get_shape_from_layout, get_strides_from_layout
 
 BLOCK_N = 64  # keys per tile: the sequence length must be a multiple of it
-HEAD_DIM = 128
+HEAD_DIMS = (64, 128)
 _DTYPES = {torch.float16: _lib.G9_F16, torch.bfloat16: _lib.G9_BF16}
 
 
@@ -21,7 +21,7 @@ def fmha_forward(q, k, v, o, metadata, scale_on_q: bool, variant: int, lse=None)
     The checks follow run_gluon_attention (kernels/attention/fmha_v4.py:761-775):
     non-causal only, K sequence length a multiple of 64, Q and K sequence
     lengths equal (assertions there and here); beyond those this kernel needs
-    head dim 128 and 16-bit tensors on one GPU (ValueError).  ``lse``, if
+    head dim 64 or 128 and 16-bit tensors on one GPU (ValueError).  ``lse``, if
     given, is a contiguous fp32 (batch, query heads, seq) tensor that receives
     each query's natural-log log-sum-exp of its scaled scores."""
     assert not metadata.causal, "the gfx950 FMHA kernel supports non-causal attention only"
@@ -29,8 +29,8 @@ def fmha_forward(q, k, v, o, metadata, scale_on_q: bool, variant: int, lse=None)
     assert metadata.max_seqlens_q == metadata.max_seqlens_k, "combined N_CTX requires Q seqlen == K seqlen"
     batch, nheads_q, nheads_k, head_size = get_shape_from_layout(q, k, metadata)
     assert head_size & (head_size - 1) == 0, "head dim must be a power of two"
-    if head_size != HEAD_DIM:
-        raise ValueError(f"head dim {head_size} unsupported: the gfx950 kernel is built for {HEAD_DIM}")
+    if head_size not in HEAD_DIMS:
+        raise ValueError(f"head dim {head_size} unsupported: the gfx950 kernels are built for {HEAD_DIMS}")
     if q.dtype not in _DTYPES or any(t.dtype != q.dtype for t in (k, v, o)):
         raise ValueError(f"q, k, v, o must share one of {list(_DTYPES)}; got {[t.dtype for t in (q, k, v, o)]}")
     dev = q.device

@@ -14,7 +14,7 @@ def run_gluon_attention(q, k, v, o, metadata: MetaData, scale_on_q: bool = True,
     into ``o`` (kernels/attention/fmha_v4.py:761-790).
 
     Non-causal self-attention, Q and K sequence lengths equal and a multiple
-    of 64, head dim 128, fp16 or bf16, ``bhsd`` or ``bshd`` layout, grouped
+    of 64, head dim 128 or 64, fp16 or bf16, ``bhsd`` or ``bshd`` layout, grouped
     K/V heads allowed.  ``scale_on_q`` folds sm_scale * log2(e) into Q before
     the loop, as the reference's SCALE_ON_Q.  ``lse`` (keyword, optional)
     receives the per-query log-sum-exp."""

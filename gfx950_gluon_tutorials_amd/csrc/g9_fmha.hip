@@ -1,15 +1,15 @@
 // Flash-attention forward (non-causal) for gfx950: O = softmax(Q K^T * sm_scale) V
 // per (batch, query head), with grouped K/V heads (query head h reads K/V head
-// h * HK / HQ).  Head dim 128, FP16 or BF16 in and out, fp32 softmax and
-// accumulation.  extern "C" entry: g9_fmha_fwd (include/gfx950_fmha.h).
+// h * HK / HQ).  Head dim 128 or 64, FP16 or BF16 in and out, fp32 softmax
+// and accumulation.  extern "C" entry: g9_fmha_fwd (include/gfx950_fmha.h).
 //
 // One workgroup owns 256 query rows of one (batch, head) and walks all keys in
 // tiles of 64.  Its 8 waves (2 per SIMD) own 32 query rows each, so every
 // row-wise reduction stays inside a wave.  Per key tile a wave runs
-//   S^T = K . Q^T    16 MFMAs 32x32x16 (two 32-key blocks x 8 steps of 16 d);
-//                    K fragments from LDS, Q fragments in registers;
+//   S^T = K . Q^T    D/8 MFMAs 32x32x16 (two 32-key blocks x D/16 steps of
+//                    16 d); K fragments from LDS, Q fragments in registers;
 //   online softmax   running max m and (lane-partial) sum l in log2 units;
-//   O^T += V^T . P^T 16 MFMAs (4 blocks of 32 d x 4 steps of 16 keys);
+//   O^T += V^T . P^T D/8 MFMAs (D/32 blocks of 32 d x 4 steps of 16 keys);
 //                    P^T straight from the S^T registers, V^T through LDS
 //                    transpose reads.
 // The scores are computed transposed (the keys are the MFMA's rows): lane l
@@ -59,7 +59,6 @@ G9_DEV void stamp(int) {}
 
 constexpr int kBlockM = 256;                // query rows per workgroup
 constexpr int kBlockN = 64;                 // keys per tile
-constexpr int kHd = 128;                    // head dim
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -198,16 +197,21 @@ G9_DEV u32x2 tr_read(u32 addr) {
 
 constexpr int kPitchK = 1024;                  // bytes between K chunk columns
 constexpr int kPitchV = 1088;                  // bytes between V chunk columns
-constexpr int kTileK = 16 * kPitchK;           // one K tile in LDS
-constexpr int kTileV = 16 * kPitchV;           // one V tile in LDS
-constexpr int kLdsV = 2 * kTileK;              // V buffers after the two K buffers
-constexpr int kLdsBytes = 2 * kTileK + 2 * kTileV;
 
 // SOQ: the scale is folded into Q, so the scores already are in log2 units
 // and the exponent argument is a 2-source subtract instead of a 3-source fma
 // (fewer register-file reads beside the other wave's LDS returns).
-template <bool BF16, bool LAZY, bool SOQ>
+template <bool BF16, bool LAZY, bool SOQ, int HD>
 struct Pipe {
+  static_assert(HD == 64 || HD == 128, "head dim 64 or 128");
+  static constexpr int kNS = HD / 16;          // QK steps of 16 head-dim values
+  static constexpr int kND = HD / 32;          // PV blocks of 32 head-dim values
+  static constexpr int kNC = HD / 8;           // 16-byte chunk columns per row = operand fragments per tile
+  static constexpr int kCW = kNC / kWaves;     // chunk columns each wave DMAs per tile (2 or 1)
+  static constexpr int kTileK = kNC * kPitchK;  // one K tile in LDS
+  static constexpr int kTileV = kNC * kPitchV;  // one V tile in LDS
+  static constexpr int kLdsV = 2 * kTileK;     // V buffers after the two K buffers
+  static constexpr int kLdsBytes = 2 * kTileK + 2 * kTileV;
   static constexpr int kE1 = G9_FMHA_VEC1_EXPS;
   const FaParams& p;
   int nt, nte, wave;  // tiles, tiles rounded up to even, wave index
@@ -216,30 +220,30 @@ struct Pipe {
   u32 voffk, voffv;  // lane's row offset in global K / V
   u32 ak, av;        // lane's LDS read base for K / V
   float sc;
-  u32x4 qf[8];
-  u32x4 kv[16];  // K_t (kv[2s + blk]: step s of 16 head-dim values, key block blk) or V_t (kv[4t + d])
-  f32x16 o[4];   // O^T, head-dim block d
+  u32x4 qf[kNS];
+  u32x4 kv[kNC];  // K_t (kv[2s + blk]: step s of 16 head-dim values, key block blk) or V_t (kv[kND t + d])
+  f32x16 o[kND];  // O^T, head-dim block d
   float m, l, alpha;
 
   G9_DEV explicit Pipe(const FaParams& pp) : p(pp) {}
 
-  // Wave w fetches chunk columns 2w and 2w + 1 of a tile.
+  // Wave w fetches chunk columns kCW w .. kCW w + kCW - 1 of a tile.
   G9_DEV void dma_k(int tile, int buf) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      dma16_untracked(rk, lds0 + buf * kTileK + (2 * wave + c) * kPitchK, voffk,
-                      (u32)tile * kBlockN * p.ldk + (2 * wave + c) * 16);
+    for (int c = 0; c < kCW; ++c)
+      dma16_untracked(rk, lds0 + buf * kTileK + (kCW * wave + c) * kPitchK, voffk,
+                      (u32)tile * kBlockN * p.ldk + (kCW * wave + c) * 16);
   }
   G9_DEV void dma_v(int tile, int buf) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      dma16_untracked(rv, lds0 + kLdsV + buf * kTileV + (2 * wave + c) * kPitchV, voffv,
-                      (u32)tile * kBlockN * p.ldv + (2 * wave + c) * 16);
+    for (int c = 0; c < kCW; ++c)
+      dma16_untracked(rv, lds0 + kLdsV + buf * kTileV + (kCW * wave + c) * kPitchV, voffv,
+                      (u32)tile * kBlockN * p.ldv + (kCW * wave + c) * 16);
   }
   template <int BUF>
   G9_DEV void read_k() {
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < kNS; ++s)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
         kv[2 * s + blk] = *(const G9_LDS u32x4*)(uintptr_t)(ak + BUF * kTileK + 2 * s * kPitchK + blk * 512);
@@ -249,11 +253,11 @@ struct Pipe {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
+      for (int d = 0; d < kND; ++d) {
         const u32 a = av + BUF * kTileV + 4 * d * kPitchV + 256 * t;
         const u32x2 lo = tr_read(a);
         const u32x2 hi = tr_read(a + 128);
-        kv[4 * t + d] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        kv[kND * t + d] = u32x4{lo.x, lo.y, hi.x, hi.y};
       }
   }
   // S^T of the tile in kv: two 32-key blocks.
@@ -261,7 +265,7 @@ struct Pipe {
     s0 = mfma<BF16>(kv[0], qf[0], f32x16{});
     s1 = mfma<BF16>(kv[1], qf[0], f32x16{});
 #pragma unroll
-    for (int s = 1; s < 8; ++s) {
+    for (int s = 1; s < kNS; ++s) {
       s0 = mfma<BF16>(kv[2 * s], qf[s], s0);
       s1 = mfma<BF16>(kv[2 * s + 1], qf[s], s1);
     }
@@ -274,7 +278,7 @@ struct Pipe {
       const u32x4 pt = t & 1 ? __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 8, 9, 10, 11))
                              : __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 0, 1, 2, 3));
 #pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] = mfma<BF16>(kv[4 * t + d], pt, o[d]);
+      for (int d = 0; d < kND; ++d) o[d] = mfma<BF16>(kv[kND * t + d], pt, o[d]);
     }
   }
   // p = 2^(x * sc - m) for score register i (0..31) of a lane: block i / 16,
@@ -355,20 +359,22 @@ struct Pipe {
     l *= alpha;
     if (!LAZY || __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+      for (int d = 0; d < kND; ++d) o[d] *= alpha;
     }
   }
 
-  // Interleave of a dot cluster: MFMA i followed by VN VALU instructions.
+  // Interleave of a dot cluster (kNC MFMAs): MFMA i followed by VN VALU
+  // instructions (twice as many at head dim 64, whose clusters have half the
+  // MFMAs for the same softmax work).
   // An MFMA 32x32x16 takes 32 cycles; about six plain VALU instructions or
   // two to three exponentials issue beside it without delaying the next one
   // (measured).
   template <int VN>
   G9_DEV static void interleave() {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kNC; ++i) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_VALU, VN, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VALU, VN * 16 / kNC, 0);
     }
   }
 
@@ -396,7 +402,7 @@ struct Pipe {
     barrier();
     // M1(j): V_j was waited for at the end of M2(j-1) (or the prologue).
     read_v<PAR>();
-    if (j + 2 < nte) waitcnt<2, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
+    if (j + 2 < nte) waitcnt<kCW, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
     if (j + 3 < nte) dma_k(j + 3, PAR ^ 1);
     if constexpr (NEXT) {
       if (j + 1 >= nt) {  // the phantom tile (a branch, not 32 selects per step)
@@ -421,13 +427,13 @@ struct Pipe {
       pv(c0, c1);
     }
 #pragma unroll
-    for (int d = 0; d < 4; ++d) pin_vec(o[d]);
+    for (int d = 0; d < kND; ++d) pin_vec(o[d]);
     barrier();
     // M2(j)
     if constexpr (NEXT) {
       read_k<PAR>();
       if (j + 3 < nte)
-        waitcnt<2, 15>();  // V_{j+1} landed (K_{j+3} may be in flight)
+        waitcnt<kCW, 15>();  // V_{j+1} landed (K_{j+3} may be in flight)
       else
         waitcnt<0, 15>();
       rescale();
@@ -438,9 +444,11 @@ struct Pipe {
   }
 };
 
-template <bool BF16, bool LAZY, bool SOQ>
-G9_DEV void fmha_fwd(const FaParams& p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+// smem: PipeT::kLdsBytes of LDS, 1024-byte aligned, declared by the kernel
+// (one array for both scale placements a kernel instantiates).
+template <bool BF16, bool LAZY, bool SOQ, int HD>
+G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
+  using PipeT = Pipe<BF16, LAZY, SOQ, HD>;
   stamp(0);
   const int total = p.B * p.HQ * p.mblocks;
   int pid, unused;
@@ -451,7 +459,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int h = lane >> 5;
 
-  Pipe<BF16, LAZY, SOQ> P(p);
+  PipeT P(p);
   P.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   P.nt = p.S / kBlockN;
   P.nte = (P.nt + 1) & ~1;
@@ -464,14 +472,14 @@ G9_DEV void fmha_fwd(const FaParams& p) {
 
   const int qrow = mb * kBlockM + wave * 32 + (lane & 31);
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
+  for (int s = 0; s < PipeT::kNS; ++s)
     P.qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (u32)qrow * p.ldq + (16 * s + 8 * h) * 2, 0, 0));
   P.voffk = (u32)lane * p.ldk;
   P.voffv = (u32)lane * p.ldv;
   P.ak = P.lds0 + h * kPitchK + (lane & 31) * 16;
   {
     const int G = lane >> 4, jj = lane & 15;
-    P.av = P.lds0 + kLdsV + (2 * (G & 1) + ((jj & 3) >> 1)) * kPitchV + (4 * (G >> 1) + (jj >> 2)) * 16 + 8 * (jj & 1);
+    P.av = P.lds0 + PipeT::kLdsV + (2 * (G & 1) + ((jj & 3) >> 1)) * kPitchV + (4 * (G >> 1) + (jj >> 2)) * 16 + 8 * (jj & 1);
   }
   // Prologue: K_0, V_0, K_1 in; S_0 and its first softmax half; K_2 and V_1
   // requested (in that order: the loop expects K_{j+2} before V_{j+1}); K_1
@@ -482,7 +490,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   P.sc = p.scale_log2;
   if constexpr (SOQ) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < PipeT::kNS; ++s)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const f32x2 x = unpack2<BF16>(P.qf[s][e]);
@@ -491,7 +499,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
     P.sc = 1.f;
   }
 #pragma unroll
-  for (int d = 0; d < 4; ++d) P.o[d] = f32x16{};
+  for (int d = 0; d < PipeT::kND; ++d) P.o[d] = f32x16{};
   P.m = -__builtin_inff();
   P.l = 0.f;
   waitcnt<0, 15>();
@@ -527,7 +535,7 @@ G9_DEV void fmha_fwd(const FaParams& p) {
   if (qrow < p.S) {
     char* orow = p.o + b * p.o_b + hq * p.o_h + (size_t)qrow * p.ldo;
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
+    for (int d = 0; d < PipeT::kND; ++d)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int col = 32 * d + 8 * r + 4 * h;
@@ -545,19 +553,25 @@ G9_DEV void fmha_fwd(const FaParams& p) {
 
 using namespace g9;
 
-// Kernels: g9_fmha_fwd_{bf16,f16}_v{3,4}; v3 rescales every tile, v4 lazily.
-#define G9_FMHA_KERNEL(NAME, BF16, LAZY)                                                                   \
+// Kernels: g9_fmha_fwd_{bf16,f16}_v{3,4}[_d64]; v3 rescales every tile, v4
+// lazily; head dim 128, or 64 with the _d64 suffix.
+#define G9_FMHA_KERNEL(NAME, BF16, LAZY, HD)                                                              \
   extern "C" __global__ __launch_bounds__(fa::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void \
   NAME(fa::FaParams p) {                                                                                  \
+    __shared__ __attribute__((aligned(1024))) char smem[fa::Pipe<BF16, LAZY, true, HD>::kLdsBytes];        \
     if (p.scale_on_q)                                                                                     \
-      fa::fmha_fwd<BF16, LAZY, true>(p);                                                                  \
+      fa::fmha_fwd<BF16, LAZY, true, HD>(p, smem);                                                        \
     else                                                                                                  \
-      fa::fmha_fwd<BF16, LAZY, false>(p);                                                                           \
+      fa::fmha_fwd<BF16, LAZY, false, HD>(p, smem);                                                       \
   }
-G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false)
-G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false)
-G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v4, true, true)
-G9_FMHA_KERNEL(g9_fmha_fwd_f16_v4, false, true)
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3, true, false, 128)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3, false, false, 128)
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v4, true, true, 128)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v4, false, true, 128)
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v3_d64, true, false, 64)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v3_d64, false, false, 64)
+G9_FMHA_KERNEL(g9_fmha_fwd_bf16_v4_d64, true, true, 64)
+G9_FMHA_KERNEL(g9_fmha_fwd_f16_v4_d64, false, true, 64)
 
 extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t HQ,
                            int64_t HK, int64_t S, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
@@ -566,7 +580,7 @@ extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o,
   if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
   if (variant != 3 && variant != 4) return G9_ERR_SCHEDULE;
   if (B <= 0 || HQ <= 0 || HK <= 0 || S <= 0 || HQ % HK != 0) return G9_ERR_SHAPE;
-  if (D != fa::kHd || S % fa::kBlockN != 0) return G9_ERR_SHAPE;
+  if ((D != 128 && D != 64) || S % fa::kBlockN != 0) return G9_ERR_SHAPE;
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return G9_ERR_LAYOUT;
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* ptr[4] = {q, k, v, o};
@@ -609,11 +623,13 @@ extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o,
   p.scale_log2 = sm_scale * fa::kLog2e;
   p.scale_on_q = scale_on_q != 0;
   void* args[] = {&p};
-  const bool bf = dtype == G9_BF16, lazy = variant == 4;
-  const void* fn = lazy ? (bf ? reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v4)
-                              : reinterpret_cast<const void*>(g9_fmha_fwd_f16_v4))
-                        : (bf ? reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v3)
-                              : reinterpret_cast<const void*>(g9_fmha_fwd_f16_v3));
+  // [head dim 64][lazy][bf16]
+  static const void* const kFns[2][2][2] = {
+      {{reinterpret_cast<const void*>(g9_fmha_fwd_f16_v3), reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v3)},
+       {reinterpret_cast<const void*>(g9_fmha_fwd_f16_v4), reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v4)}},
+      {{reinterpret_cast<const void*>(g9_fmha_fwd_f16_v3_d64), reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v3_d64)},
+       {reinterpret_cast<const void*>(g9_fmha_fwd_f16_v4_d64), reinterpret_cast<const void*>(g9_fmha_fwd_bf16_v4_d64)}}};
+  const void* fn = kFns[D == 64][variant == 4][dtype == G9_BF16];
   return hipLaunchKernel(fn, dim3((unsigned)(B * HQ * mblocks)), dim3(fa::kThreads), args, 0,
                          reinterpret_cast<hipStream_t>(stream)) == hipSuccess
              ? G9_OK

@@ -6,8 +6,8 @@
  * O = softmax(Q K^T * sm_scale) V for every (batch, query head), non-causal,
  * with grouped K/V heads: query head h reads K/V head h * HK / HQ (HQ a
  * multiple of HK; HK == HQ is plain multi-head, HK == 1 multi-query).  Q, K, V
- * and O hold 16-bit elements (`dtype` G9_F16 or G9_BF16) with head dim 128;
- * scores, softmax and the output accumulator are fp32.
+ * and O hold 16-bit elements (`dtype` G9_F16 or G9_BF16) with head dim 128
+ * or 64; scores, softmax and the output accumulator are fp32.
  */
 #ifndef GFX950_FMHA_H
 #define GFX950_FMHA_H
@@ -30,7 +30,8 @@ extern "C" {
  * ELEMENTS given as (batch, head, seq, dim) -- the order of
  * get_strides_from_layout (kernels/attention/common.py:84-92), so both the
  * bhsd and the bshd layouts (and any other with a unit dim stride) are
- * accepted.  Requirements: D == 128, S a multiple of 64, unit dim stride,
+ * accepted.  Requirements: D == 128 or D == 64 (the reference's powers of
+ * two; its layouts are written for 128), S a multiple of 64, unit dim stride,
  * 16-byte aligned base pointers and batch / head / seq strides, and
  * (S + 256) * seq_stride * 2 < 2^31 bytes for each tensor.
  *

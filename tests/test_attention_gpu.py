@@ -4,10 +4,10 @@ reference's acceptance rule (kernels/attention/common.py:142-171):
 |o - o_ref| <= atol + 1e-3 |o_ref| with atol = max(1e-3, 2 eps(out) max|o_ref|).
 
 Cases: both input types, both layouts, both rescale variants, scale on Q or
-on the scores, grouped K/V heads (MHA, GQA, MQA), sequence lengths that leave
-a partial 256-query block, strided views, extreme score ranges, the
-log-sum-exp output, determinism, and the benchmark shape checked on sampled
-rows.
+on the scores, head dims 128 and 64, grouped K/V heads (MHA, GQA, MQA),
+sequence lengths that leave a partial 256-query block, strided views, extreme
+score ranges, the log-sum-exp output, determinism, and the benchmark shape
+checked on sampled rows.
 """
 
 import math
@@ -26,12 +26,12 @@ DT_NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
 RUN = {3: fmha_v3.run_gluon_attention, 4: fmha_v4.run_gluon_attention}
 
 
-def _inputs(B, HQ, HK, S, dtype, layout, seed, scale=1.0):
+def _inputs(B, HQ, HK, S, dtype, layout, seed, scale=1.0, D=128):
     g = torch.Generator().manual_seed(seed)
-    shp = (lambda h: (B, h, S, 128)) if layout == "bhsd" else (lambda h: (B, S, h, 128))
+    shp = (lambda h: (B, h, S, D)) if layout == "bhsd" else (lambda h: (B, S, h, D))
     q, k, v = (torch.randn(shp(h), generator=g) * sc for h, sc in ((HQ, scale), (HK, 1.0), (HK, 1.0)))
     q, k, v = (t.to(dtype) for t in (q, k, v))
-    md = MetaData(sm_scale=128**-0.5)
+    md = MetaData(sm_scale=D**-0.5)
     md.max_seqlens_q = md.max_seqlens_k = S
     md.layout = layout
     return q, k, v, md
@@ -80,6 +80,45 @@ def test_head_groupings_and_lengths(gpu, B, HQ, HK, S, dtype):
     q, k, v, md = _inputs(B, HQ, HK, S, DT[dtype], "bhsd", seed=S + HQ)
     o, L = _run(q, k, v, md, gpu)
     _check(o, L, q, k, v, md)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("variant", [3, 4])
+@pytest.mark.parametrize("scale_on_q", [True, False])
+def test_head_dim_64(gpu, dtype, layout, variant, scale_on_q):
+    # Head dim 64: half the MFMAs per tile, one DMA per operand per wave.
+    q, k, v, md = _inputs(2, 4, 2, 320, DT[dtype], layout, seed=21, D=64)
+    o, L = _run(q, k, v, md, gpu, variant, scale_on_q)
+    _check(o, L, q, k, v, md)
+
+
+@pytest.mark.parametrize("B,HQ,HK,S,qscale", [(1, 8, 1, 1024, 1.0), (2, 3, 3, 576, 1.0), (1, 2, 2, 512, 16.0),
+                                              (1, 1, 1, 64, 1.0)])
+def test_head_dim_64_groupings_lengths_and_ranges(gpu, B, HQ, HK, S, qscale):
+    q, k, v, md = _inputs(B, HQ, HK, S, torch.bfloat16, "bhsd", seed=S + 7 * HQ, scale=qscale, D=64)
+    for variant in (3, 4):
+        o, L = _run(q, k, v, md, gpu, variant, scale_on_q=False)
+        _check(o, L, q, k, v, md)
+
+
+def test_head_dim_64_strided_views(gpu):
+    # bshd views of one packed (B, S, 3, H, 64) buffer; the output a view with a
+    # padded head stride whose padding must stay untouched.
+    B, S, H = 2, 448, 3
+    g = torch.Generator().manual_seed(22)
+    qkv = torch.randn(B, S, 3, H, 64, generator=g).to(torch.float16)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    md = MetaData(sm_scale=64**-0.5)
+    md.max_seqlens_q = md.max_seqlens_k = S
+    md.layout = "bshd"
+    big = torch.full((B, S, H, 72), float("nan"), dtype=torch.float16, device=gpu)
+    o = big[..., :64]
+    qkv_d = qkv.to(gpu)
+    fmha_v4.run_gluon_attention(qkv_d[:, :, 0], qkv_d[:, :, 1], qkv_d[:, :, 2], o, md)
+    torch.cuda.synchronize()
+    _check(o.cpu(), None, q, k, v, md)
+    assert torch.isnan(big[..., 64:].cpu().float()).all(), "wrote past the output view"
 
 
 @pytest.mark.parametrize("variant", [3, 4])

@@ -180,8 +180,11 @@ def test_drop_in_rejects_what_the_reference_asserts_and_more():
     q, k, v, o, md = _case(D=96)
     with pytest.raises(AssertionError):  # not a power of two
         fmha_v3.run_gluon_attention(q, k, v, o, md)
-    q, k, v, o, md = _case(D=64)
+    q, k, v, o, md = _case(D=32)
     with pytest.raises(ValueError, match="head dim"):
+        run_gluon_attention(q, k, v, o, md)
+    q, k, v, o, md = _case(D=64)
+    with pytest.raises(ValueError, match="GPU"):  # head dim 64 is accepted; CPU tensors are not
         run_gluon_attention(q, k, v, o, md)
     q, k, v, o, md = _case(dtype=torch.float32)
     with pytest.raises(ValueError):
@@ -212,7 +215,8 @@ def _call(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(dtype=_lib.G9_BF8), _lib.G9_ERR_DTYPE),
     (dict(variant=5), _lib.G9_ERR_SCHEDULE),
-    (dict(D=64), _lib.G9_ERR_SHAPE),
+    (dict(D=32), _lib.G9_ERR_SHAPE),
+    (dict(D=256), _lib.G9_ERR_SHAPE),
     (dict(S=100), _lib.G9_ERR_SHAPE),
     (dict(S=0), _lib.G9_ERR_SHAPE),
     (dict(HQ=3, HK=2), _lib.G9_ERR_SHAPE),
