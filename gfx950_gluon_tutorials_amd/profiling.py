@@ -50,9 +50,10 @@ REALTIME_HZ = 100e6
 NUM_XCDS = 8
 
 
-def phase_stats(stamps: np.ndarray, stages: int) -> dict:
+def phase_stats(stamps: np.ndarray, stages: int, cycles_per_stage: int = CYCLES_PER_STAGE) -> dict:
     """Summarises raw stamps (workgroups x 8 uint64: clock/realtime pairs at
-    entry, loop start, loop end, end) into medians and spreads."""
+    entry, loop start, loop end, end) into medians and spreads; the ideal loop
+    is stages x cycles_per_stage MFMA cycles per SIMD."""
     d = np.asarray(stamps, dtype=np.int64).reshape(-1, 8)
     t = d[:, 0::2]
     r = d[:, 1::2]
@@ -63,7 +64,7 @@ def phase_stats(stamps: np.ndarray, stages: int) -> dict:
     if (ticks <= 0).any() or (loop <= 0).any():
         raise ValueError("stamps are not increasing: was the last launch a DP launch of the timing build?")
     clock = (t[:, 3] - t[:, 0]) / (ticks / REALTIME_HZ)
-    ideal = stages * CYCLES_PER_STAGE
+    ideal = stages * cycles_per_stage
     loop_med = float(np.median(loop))
     # Workgroups are dispatched round-robin over the XCDs (workgroup i runs on
     # XCD i % 8 of an MI355X); each XCD runs at its own clock.
@@ -182,12 +183,11 @@ def measure(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.
     return out
 
 
-def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s: float = 0.8) -> dict:
+def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s: float = 0.8, D: int = 128) -> dict:
     """Phase statistics of one flash-attention launch (g9_fmha_fwd, bhsd,
-    head dim 128) at steady state, as ``measure``.  The loop covers all key
-    tiles of 64 (an even count); each costs 2048 ideal MFMA cycles per SIMD
-    (2 waves x 32 MFMAs 32x32x16 x 32 cycles), so phase_stats applies with
-    stages = tiles."""
+    head dim D = 128 or 64) at steady state, as ``measure``.  The loop covers
+    all key tiles of 64 (an even count); each costs 2048 * D / 128 ideal MFMA
+    cycles per SIMD (2 waves x D / 4 MFMAs 32x32x16 x 32 cycles)."""
     import ctypes
     import time
 
@@ -203,9 +203,9 @@ def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s:
     dev = torch.device("cuda:0")
     tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
     g = torch.Generator().manual_seed(0)
-    q, k, v = ((torch.randn(B, H, S, 128, generator=g)).to(tdt).to(dev) for _ in range(3))
+    q, k, v = ((torch.randn(B, H, S, D, generator=g)).to(tdt).to(dev) for _ in range(3))
     o = torch.empty_like(q)
-    md = MetaData(sm_scale=128**-0.5)
+    md = MetaData(sm_scale=D**-0.5)
     md.max_seqlens_q = md.max_seqlens_k = S
     md.layout = "bhsd"
     fn = fmha_v4.run_gluon_attention if variant == 4 else fmha_v3.run_gluon_attention
@@ -228,9 +228,9 @@ def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s:
     buf = np.zeros(n * 8, dtype=np.uint64)
     _lib.check(lib.g9_fmha_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_fmha_timing_read")
     tiles = (S // 64 + 1) // 2 * 2
-    out = phase_stats(buf, tiles)
-    out.update({"kernel": f"fmha_v{variant}", "dtype": dtype, "B": B, "H": H, "S": S, "launch_us": round(launch_us, 2),
-                "tflops": round(compute_flops(B, H, S, S, 128, False) / launch_us / 1e6, 1)})
+    out = phase_stats(buf, tiles, CYCLES_PER_STAGE * D // 128)
+    out.update({"kernel": f"fmha_v{variant}", "dtype": dtype, "B": B, "H": H, "S": S, "D": D,
+                "launch_us": round(launch_us, 2), "tflops": round(compute_flops(B, H, S, S, D, False) / launch_us / 1e6, 1)})
     return out
 
 
@@ -402,7 +402,7 @@ def main(argv=None) -> int:
     ap.add_argument("--json", help="also write the results to this file")
     ap.add_argument("--streamk", action="store_true",
                     help="stream-K fixup cost instead (give --M/--N/--K; e.g. 8192 1280 8192)")
-    ap.add_argument("--fmha", help="flash-attention forward instead: B,H,S (e.g. 32,8,8192); "
+    ap.add_argument("--fmha", help="flash-attention forward instead: B,H,S[,D] (e.g. 32,8,8192; D 128 or 64); "
                     "--dtypes fp16/bf16, --waves is ignored")
     ap.add_argument("--variants", default="4", help="with --fmha: 3, 4 or 3,4")
     ap.add_argument("--operands", help="FP16 launch time per operand distribution instead "
@@ -410,12 +410,13 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     results = []
     if args.fmha:
-        B, H, S = (int(x) for x in args.fmha.split(","))
+        B, H, S, *rest = (int(x) for x in args.fmha.split(","))
+        D = rest[0] if rest else 128
         for dt in args.dtypes.split(","):
             for var in (int(x) for x in args.variants.split(",")):
-                r = measure_fmha(dt, B, H, S, var)
+                r = measure_fmha(dt, B, H, S, var, D=D)
                 results.append(r)
-                print(f"fmha_v{var} {dt} B={B} H={H} S={S} D=128: {r['launch_us']:.1f} us/launch "
+                print(f"fmha_v{var} {dt} B={B} H={H} S={S} D={D}: {r['launch_us']:.1f} us/launch "
                       f"({r['tflops']:.0f} TFLOPS)  loop MFMA eff {r['mfma_efficiency']:.3f}  clock "
                       f"{r['clock_ghz']:.3f} GHz  prologue {r['prologue_cycles']}  loop {r['loop_cycles']} (ideal "
                       f"{r['ideal_loop_cycles']})  epilogue {r['epilogue_cycles']} cycles | workgroup "
