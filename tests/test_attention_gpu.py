@@ -74,7 +74,7 @@ def test_small_problems(gpu, dtype, layout, variant, scale_on_q):
 
 
 @pytest.mark.parametrize("B,HQ,HK,S", [(1, 8, 8, 1024), (1, 4, 1, 2048), (3, 2, 2, 64), (1, 1, 1, 256),
-                                       (2, 6, 3, 576)])
+                                       (2, 6, 3, 576), (1, 2, 1, 128), (1, 2, 2, 192)])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_head_groupings_and_lengths(gpu, B, HQ, HK, S, dtype):
     q, k, v, md = _inputs(B, HQ, HK, S, DT[dtype], "bhsd", seed=S + HQ)
@@ -94,7 +94,7 @@ def test_head_dim_64(gpu, dtype, layout, variant, scale_on_q):
 
 
 @pytest.mark.parametrize("B,HQ,HK,S,qscale", [(1, 8, 1, 1024, 1.0), (2, 3, 3, 576, 1.0), (1, 2, 2, 512, 16.0),
-                                              (1, 1, 1, 64, 1.0)])
+                                              (1, 1, 1, 64, 1.0), (1, 2, 1, 128, 1.0), (1, 2, 2, 192, 4.0)])
 def test_head_dim_64_groupings_lengths_and_ranges(gpu, B, HQ, HK, S, qscale):
     q, k, v, md = _inputs(B, HQ, HK, S, torch.bfloat16, "bhsd", seed=S + 7 * HQ, scale=qscale, D=64)
     for variant in (3, 4):
