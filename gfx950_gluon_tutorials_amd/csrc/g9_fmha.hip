@@ -171,6 +171,9 @@ G9_DEV u32x2 tr_read(u32 addr) {
 // Waves 4-7 run one cluster behind waves 0-3, so on every SIMD one wave is in
 // a dot cluster (MFMA + VALU) while the other is in a memory cluster: the
 // matrix pipe, the VALU and the LDS / memory pipe are busy at the same time.
+// Memory clusters run at wave priority 1, dot clusters at 0, so the memory
+// wave's reads, DMAs and rescale win issue arbitration (measured: 2.5% fewer
+// loop cycles with the lazy rescale; the priority of M2 is what matters).
 // K and V tiles are double buffered in LDS (tile t in buffer t & 1); each DMA
 // is waited for (by its own wave, then a barrier) one cluster before the tile
 // is read, which gives it about one and a half loop iterations to land.
@@ -389,6 +392,7 @@ struct Pipe {
   template <int PAR, bool NEXT>
   G9_DEV void step(int j, f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
     // D1(j)
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (NEXT) {
       qk(n0, n1);
       vec2(c0, c1);
@@ -401,6 +405,7 @@ struct Pipe {
     pin_p(c0, c1);
     barrier();
     // M1(j): V_j was waited for at the end of M2(j-1) (or the prologue).
+    __builtin_amdgcn_s_setprio(1);
     read_v<PAR>();
     if (j + 2 < nte) waitcnt<kCW, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
     if (j + 3 < nte) dma_k(j + 3, PAR ^ 1);
@@ -417,6 +422,7 @@ struct Pipe {
     waitcnt<63, 0>();
     barrier();
     // D2(j)
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (NEXT) {
       pv(c0, c1);
       vec1(n0, n1);
@@ -430,6 +436,7 @@ struct Pipe {
     for (int d = 0; d < kND; ++d) pin_vec(o[d]);
     barrier();
     // M2(j)
+    __builtin_amdgcn_s_setprio(1);
     if constexpr (NEXT) {
       read_k<PAR>();
       if (j + 3 < nte)
@@ -527,6 +534,7 @@ G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
   }
   P.template step<0, true>(j, sa0, sa1, sb0, sb1);
   P.template step<1, false>(j + 1, sb0, sb1, sa0, sa1);
+  __builtin_amdgcn_s_setprio(0);
   if (!lag) barrier();
   stamp(2);
 
