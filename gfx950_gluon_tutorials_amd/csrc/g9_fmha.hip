@@ -161,13 +161,14 @@ G9_DEV u32x2 tr_read(u32 addr) {
 // clusters, each closed by a workgroup barrier:
 //   D1(j)  QK MFMAs of tile j+1 (K_{j+1} from registers) and, in their issue
 //          shadow, the second half of tile j's softmax (the remaining
-//          exponentials, P_j to 16 bit, the row sum);
+//          exponentials, P_j to 16 bit, the row sum) and, with the eager
+//          rescale, half of O's rescale for tile j;
 //   M1(j)  LDS reads of V_j; DMA of K_{j+3}; tile j+1's row max, new running
 //          max and rescale factor (a dependent chain: it would stall MFMA
 //          issue in a dot cluster, here it fills the idle VALU);
 //   D2(j)  PV MFMAs of tile j and, in their shadow, most of tile j+1's
 //          exponentials;
-//   M2(j)  LDS reads of K_{j+2}; DMA of V_{j+2}; rescale of O and l.
+//   M2(j)  LDS reads of K_{j+2}; DMA of V_{j+2}; rescale of l and (the rest of) O.
 // Waves 4-7 run one cluster behind waves 0-3, so on every SIMD one wave is in
 // a dot cluster (MFMA + VALU) while the other is in a memory cluster: the
 // matrix pipe, the VALU and the LDS / memory pipe are busy at the same time.
@@ -190,6 +191,9 @@ G9_DEV u32x2 tr_read(u32 addr) {
 
 #ifndef G9_FMHA_VN1
 #define G9_FMHA_VN1 4  // VALU instructions after each QK MFMA of D1
+#endif
+#ifndef G9_FMHA_VN1_EAGER
+#define G9_FMHA_VN1_EAGER 6  // the same with the eager rescale's share of O in D1
 #endif
 #ifndef G9_FMHA_VN2
 #define G9_FMHA_VN2 4  // VALU instructions after each PV MFMA of D2
@@ -358,12 +362,22 @@ struct Pipe {
     }
     pin(l);
   }
+  // The eager rescale (every tile) at head dim 128 splits O: the first kSplit
+  // head-dim blocks are rescaled in the next dot cluster, as VALU work beside
+  // the QK MFMAs (rescale_early), the rest here (measured: 7.5% fewer loop
+  // cycles than all of it here; at head dim 64, whose dot clusters have half
+  // the MFMAs, 1.5% more).  The lazy rescale is rare and stays here whole.
+  static constexpr int kSplit = LAZY || HD != 128 ? 0 : kND / 2;
   G9_DEV void rescale() {
     l *= alpha;
     if (!LAZY || __builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int d = 0; d < kND; ++d) o[d] *= alpha;
+      for (int d = kSplit; d < kND; ++d) o[d] *= alpha;
     }
+  }
+  G9_DEV void rescale_early() {
+#pragma unroll
+    for (int d = 0; d < kSplit; ++d) o[d] *= alpha;
   }
 
   // Interleave of a dot cluster (kNC MFMAs): MFMA i followed by VN VALU
@@ -396,12 +410,16 @@ struct Pipe {
     if constexpr (NEXT) {
       qk(n0, n1);
       vec2(c0, c1);
-      interleave<G9_FMHA_VN1>();
+      rescale_early();
+      interleave<(kSplit ? G9_FMHA_VN1_EAGER : G9_FMHA_VN1)>();
       pin_vec(n0);
       pin_vec(n1);
     } else {
       vec2(c0, c1);
+      rescale_early();
     }
+#pragma unroll
+    for (int d = 0; d < kSplit; ++d) pin_vec(o[d]);
     pin_p(c0, c1);
     barrier();
     // M1(j): V_j was waited for at the end of M2(j-1) (or the prologue).
