@@ -85,6 +85,7 @@ enum : int {
   SG_VMEM_RD = 0x20,
   SG_DS_RD = 0x100,
   SG_DS_WR = 0x200,
+  SG_TRANS = 0x400,  // transcendental (v_exp, v_log, ...): not in SG_VALU
 };
 
 // XCD-aware tile remap followed by a GROUP_SIZE_M swizzle.  Workgroups are

@@ -58,7 +58,6 @@ G9_DEV void stamp(int) {}
 #endif
 
 constexpr int kBlockM = 256;                // query rows per workgroup
-constexpr int kBlockN = 64;                 // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -180,7 +179,7 @@ G9_DEV u32x2 tr_read(u32 addr) {
 // is read, which gives it about one and a half loop iterations to land.
 //
 // LDS tiles are stored column-major in 16-byte chunks: chunk c (head-dim
-// values 8c..8c+7) of all 64 rows is one contiguous KiB (one DMA: lane i
+// values 8c..8c+7) of all kBN rows is contiguous (one DMA per 64 rows: lane i
 // fetches row i), chunk columns kPitchK / kPitchV bytes apart.  Every LDS read
 // address is then one per-lane base register plus an immediate: K reads
 // (row = lane % 32 (+32), chunk 2s + lane / 32) cover 256 contiguous bytes per
@@ -202,63 +201,99 @@ G9_DEV u32x2 tr_read(u32 addr) {
 #define G9_FMHA_VEC1_EXPS 22  // exponentials of a tile done in D2 (of 32 per lane); the rest in D1
 #endif
 
-constexpr int kPitchK = 1024;                  // bytes between K chunk columns
-constexpr int kPitchV = 1088;                  // bytes between V chunk columns
+#ifndef G9_FMHA_VN1_64
+#define G9_FMHA_VN1_64 8  // head dim 64 (128-key tiles): VALU after each QK MFMA of D1
+#endif
+#ifndef G9_FMHA_VN2_64
+#define G9_FMHA_VN2_64 8  // head dim 64: VALU after each PV MFMA of D2
+#endif
+#ifndef G9_FMHA_VEC1_EXPS_64
+#define G9_FMHA_VEC1_EXPS_64 44  // head dim 64: exponentials of a tile (of 64 per lane) done in D2
+#endif
 
 // SOQ: the scale is folded into Q, so the scores already are in log2 units
 // and the exponent argument is a 2-source subtract instead of a 3-source fma
 // (fewer register-file reads beside the other wave's LDS returns).
+//
+// Key tiles are kBN = 8192 / HD keys: 64 at head dim 128, 128 at head dim 64,
+// so a dot cluster holds 16 MFMAs either way and the two head dims share the
+// per-cluster costs (barriers, the row-max chain, waits) over the same MFMA
+// work.  A tile's scores are kNB blocks of 32 keys (Sc).
+constexpr int sum16(const int (&a)[16]) {
+  int t = 0;
+  for (int i = 0; i < 16; ++i) t += a[i];
+  return t;
+}
+
 template <bool BF16, bool LAZY, bool SOQ, int HD>
 struct Pipe {
   static_assert(HD == 64 || HD == 128, "head dim 64 or 128");
+  static constexpr int kBN = 8192 / HD;        // keys per tile
+  static constexpr int kNB = kBN / 32;         // 32-key score blocks per tile
+  static constexpr int kKS = kBN / 16;         // PV steps of 16 keys
   static constexpr int kNS = HD / 16;          // QK steps of 16 head-dim values
   static constexpr int kND = HD / 32;          // PV blocks of 32 head-dim values
-  static constexpr int kNC = HD / 8;           // 16-byte chunk columns per row = operand fragments per tile
-  static constexpr int kCW = kNC / kWaves;     // chunk columns each wave DMAs per tile (2 or 1)
+  static constexpr int kNC = HD / 8;           // 16-byte chunk columns per row
+  static constexpr int kNF = kNS * kNB;        // K (or V) fragments per tile = MFMAs per dot cluster
+  static constexpr int kRH = kBN / 64;         // 64-row halves of a chunk column (one DMA each)
+  static constexpr int kDW = kNC * kRH / kWaves;  // DMAs per wave per operand and tile
+  static constexpr int kPitchK = kBN * 16;     // bytes between K chunk columns
+  static constexpr int kPitchV = kBN * 16 + 64;  // bytes between V chunk columns (pad: distinct banks)
   static constexpr int kTileK = kNC * kPitchK;  // one K tile in LDS
   static constexpr int kTileV = kNC * kPitchV;  // one V tile in LDS
   static constexpr int kLdsV = 2 * kTileK;     // V buffers after the two K buffers
   static constexpr int kLdsBytes = 2 * kTileK + 2 * kTileV;
-  static constexpr int kE1 = G9_FMHA_VEC1_EXPS;
+  static constexpr int kE1 = HD == 128 ? G9_FMHA_VEC1_EXPS : G9_FMHA_VEC1_EXPS_64;
+  static constexpr int kVN1 = HD == 128 ? G9_FMHA_VN1 : G9_FMHA_VN1_64;
+  static constexpr int kVN2 = HD == 128 ? G9_FMHA_VN2 : G9_FMHA_VN2_64;
+  static_assert(kNF == 16 && kKS * kND == 16, "16 MFMAs per dot cluster");
+  struct Sc {
+    f32x16 b[kNB];
+  };
   const FaParams& p;
-  int nt, nte, wave;  // tiles, tiles rounded up to even, wave index
+  int nt, nte, nfull, wave;  // tiles, tiles rounded up to even, whole tiles, wave index
   u32 lds0;
   rsrc_t rk, rv;
   u32 voffk, voffv;  // lane's row offset in global K / V
   u32 ak, av;        // lane's LDS read base for K / V
   float sc;
   u32x4 qf[kNS];
-  u32x4 kv[kNC];  // K_t (kv[2s + blk]: step s of 16 head-dim values, key block blk) or V_t (kv[kND t + d])
+  u32x4 kv[kNF];  // K_t (kv[kNB s + blk]: step s of 16 head-dim values, key block blk) or V_t (kv[kND t + d])
   f32x16 o[kND];  // O^T, head-dim block d
   float m, l, alpha;
 
   G9_DEV explicit Pipe(const FaParams& pp) : p(pp) {}
 
-  // Wave w fetches chunk columns kCW w .. kCW w + kCW - 1 of a tile.
+  // DMA q = kDW w + i of wave w covers chunk column q / kRH, rows 64 (q % kRH)
+  // .. +63 of a tile: lane i fetches row 64 (q % kRH) + i.
   G9_DEV void dma_k(int tile, int buf) {
 #pragma unroll
-    for (int c = 0; c < kCW; ++c)
-      dma16_untracked(rk, lds0 + buf * kTileK + (kCW * wave + c) * kPitchK, voffk,
-                      (u32)tile * kBlockN * p.ldk + (kCW * wave + c) * 16);
+    for (int i = 0; i < kDW; ++i) {
+      const int q = kDW * wave + i, c = q / kRH, r = q % kRH;
+      dma16_untracked(rk, lds0 + buf * kTileK + c * kPitchK + r * 1024, voffk,
+                      ((u32)tile * kBN + 64 * r) * p.ldk + c * 16);
+    }
   }
   G9_DEV void dma_v(int tile, int buf) {
 #pragma unroll
-    for (int c = 0; c < kCW; ++c)
-      dma16_untracked(rv, lds0 + kLdsV + buf * kTileV + (kCW * wave + c) * kPitchV, voffv,
-                      (u32)tile * kBlockN * p.ldv + (kCW * wave + c) * 16);
+    for (int i = 0; i < kDW; ++i) {
+      const int q = kDW * wave + i, c = q / kRH, r = q % kRH;
+      dma16_untracked(rv, lds0 + kLdsV + buf * kTileV + c * kPitchV + r * 1024, voffv,
+                      ((u32)tile * kBN + 64 * r) * p.ldv + c * 16);
+    }
   }
   template <int BUF>
   G9_DEV void read_k() {
 #pragma unroll
     for (int s = 0; s < kNS; ++s)
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
-        kv[2 * s + blk] = *(const G9_LDS u32x4*)(uintptr_t)(ak + BUF * kTileK + 2 * s * kPitchK + blk * 512);
+      for (int blk = 0; blk < kNB; ++blk)
+        kv[kNB * s + blk] = *(const G9_LDS u32x4*)(uintptr_t)(ak + BUF * kTileK + 2 * s * kPitchK + blk * 512);
   }
   template <int BUF>
   G9_DEV void read_v() {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < kKS; ++t)
 #pragma unroll
       for (int d = 0; d < kND; ++d) {
         const u32 a = av + BUF * kTileV + 4 * d * kPitchV + 256 * t;
@@ -267,53 +302,70 @@ struct Pipe {
         kv[kND * t + d] = u32x4{lo.x, lo.y, hi.x, hi.y};
       }
   }
-  // S^T of the tile in kv: two 32-key blocks.
-  G9_DEV void qk(f32x16& s0, f32x16& s1) {
-    s0 = mfma<BF16>(kv[0], qf[0], f32x16{});
-    s1 = mfma<BF16>(kv[1], qf[0], f32x16{});
+  // S^T of the tile in kv: kNB 32-key blocks.
+  G9_DEV void qk(Sc& S) {
 #pragma unroll
-    for (int s = 1; s < kNS; ++s) {
-      s0 = mfma<BF16>(kv[2 * s], qf[s], s0);
-      s1 = mfma<BF16>(kv[2 * s + 1], qf[s], s1);
-    }
+    for (int blk = 0; blk < kNB; ++blk) S.b[blk] = mfma<BF16>(kv[blk], qf[0], f32x16{});
+#pragma unroll
+    for (int s = 1; s < kNS; ++s)
+#pragma unroll
+      for (int blk = 0; blk < kNB; ++blk) S.b[blk] = mfma<BF16>(kv[kNB * s + blk], qf[s], S.b[blk]);
   }
-  // O^T += V^T P^T; P in 16 bit as vec2 left it in (s0, s1).
-  G9_DEV void pv(const f32x16& s0, const f32x16& s1) {
+  // O^T += V^T P^T; P in 16 bit as vec2 left it in S.
+  G9_DEV void pv(const Sc& S) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f32x16& sv = t < 2 ? s0 : s1;
+    for (int t = 0; t < kKS; ++t) {
+      const f32x16& sv = S.b[t / 2];
       const u32x4 pt = t & 1 ? __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 8, 9, 10, 11))
                              : __builtin_bit_cast(u32x4, __builtin_shufflevector(sv, sv, 0, 1, 2, 3));
 #pragma unroll
       for (int d = 0; d < kND; ++d) o[d] = mfma<BF16>(kv[kND * t + d], pt, o[d]);
     }
   }
-  // p = 2^(x * sc - m) for score register i (0..31) of a lane: block i / 16,
-  // register i % 16.
-  G9_DEV void expo(f32x16& s0, f32x16& s1, int i) const {
-    if (i < 16)
-      s0[i] = __builtin_amdgcn_exp2f(SOQ ? s0[i] - m : __builtin_fmaf(s0[i], sc, -m));
-    else
-      s1[i - 16] = __builtin_amdgcn_exp2f(SOQ ? s1[i - 16] - m : __builtin_fmaf(s1[i - 16], sc, -m));
+  // p = 2^(x * sc - m) for score register i (0 .. 16 kNB - 1) of a lane:
+  // block i / 16, register i % 16.
+  G9_DEV void expo(Sc& S, int i) const {
+    f32x16& v = S.b[i / 16];
+    v[i % 16] = __builtin_amdgcn_exp2f(SOQ ? v[i % 16] - m : __builtin_fmaf(v[i % 16], sc, -m));
+  }
+  // Keys past the sequence end (the phantom tile, or the second half of a
+  // 128-key tile when S is an odd multiple of 64) score -inf: their K rows
+  // were read as zeros.  `valid` = keys of the tile before the end (a
+  // multiple of 64, <= 0 for the phantom).
+  G9_DEV void mask(Sc& S, int valid) const {
+    const int from = kBN == 64 || valid <= 0 ? 0 : kNB / 2;  // whole-tile stores, no selects
+#pragma unroll
+    for (int blk = 0; blk < kNB; ++blk)
+      if (blk >= from) S.b[blk] = f32x16{} - __builtin_inff();
   }
 
   // Start of a tile's softmax: row max, running max and alpha (a dependent
   // chain ending in a cross-lane exchange; run in a memory cluster, where the
   // VALU is otherwise idle, so the MFMA shadows keep only independent work).
-  G9_DEV void vec0(f32x16& s0, f32x16& s1) {
-    float a = __builtin_fmaxf(__builtin_fmaxf(s0[0], s0[1]), s0[2]);
-    float b = __builtin_fmaxf(__builtin_fmaxf(s0[8], s0[9]), s0[10]);
-    float c = __builtin_fmaxf(__builtin_fmaxf(s1[0], s1[1]), s1[2]);
-    float d = __builtin_fmaxf(__builtin_fmaxf(s1[8], s1[9]), s1[10]);
+  // One max3 chain per 8-register half block, then a tree over the chains.
+  G9_DEV void vec0(Sc& S) {
+    float c[2 * kNB];
+#pragma unroll
+    for (int h = 0; h < 2 * kNB; ++h) {
+      const f32x16& v = S.b[h / 2];
+      const int o8 = 8 * (h & 1);
+      c[h] = __builtin_fmaxf(__builtin_fmaxf(v[o8], v[o8 + 1]), v[o8 + 2]);
+    }
 #pragma unroll
     for (int i = 3; i < 8; i += 2) {
       const int i1 = i + 1 < 8 ? i + 1 : i;
-      a = __builtin_fmaxf(__builtin_fmaxf(a, s0[i]), s0[i1]);
-      b = __builtin_fmaxf(__builtin_fmaxf(b, s0[8 + i]), s0[8 + i1]);
-      c = __builtin_fmaxf(__builtin_fmaxf(c, s1[i]), s1[i1]);
-      d = __builtin_fmaxf(__builtin_fmaxf(d, s1[8 + i]), s1[8 + i1]);
+#pragma unroll
+      for (int h = 0; h < 2 * kNB; ++h) {
+        const f32x16& v = S.b[h / 2];
+        const int o8 = 8 * (h & 1);
+        c[h] = __builtin_fmaxf(__builtin_fmaxf(c[h], v[o8 + i]), v[o8 + i1]);
+      }
     }
-    float mx = __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+#pragma unroll
+    for (int w = 2 * kNB; w > 1; w /= 2)
+#pragma unroll
+      for (int h = 0; h < w / 2; ++h) c[h] = __builtin_fmaxf(c[2 * h], c[2 * h + 1]);
+    float mx = c[0];
     mx = xhalf(mx, [](float x, float y) { return __builtin_fmaxf(x, y); });
     const float mt = SOQ ? mx : mx * sc;
     const float m_new = LAZY ? (mt - m > kLazyThreshold ? mt : m) : __builtin_fmaxf(m, mt);
@@ -321,9 +373,9 @@ struct Pipe {
     m = m_new;
   }
   // First kE1 exponentials of a tile (in place).
-  G9_DEV void vec1(f32x16& s0, f32x16& s1) {
+  G9_DEV void vec1(Sc& S) {
 #pragma unroll
-    for (int i = 0; i < kE1; ++i) expo(s0, s1, i);
+    for (int i = 0; i < kE1; ++i) expo(S, i);
   }
   // Second half: the remaining exponentials, l += row sum (fp32, before
   // rounding), P to 16 bit.  The 16-bit pairs of PV step t are written over
@@ -332,35 +384,48 @@ struct Pipe {
   // plain adds: v_dot2c on the packed values would take half the
   // instructions but does not issue beside an MFMA -- measured: two per MFMA
   // stretch its 32-cycle interval to 53.)
-  G9_DEV void vec2(f32x16& s0, f32x16& s1) {
+  G9_DEV void vec2(Sc& S) {
 #pragma unroll
-    for (int i = kE1; i < 32; ++i) expo(s0, s1, i);
-    float r0 = s0[0] + s0[1], r1 = s0[8] + s0[9], r2 = s1[0] + s1[1], r3 = s1[8] + s1[9];
+    for (int i = kE1; i < 16 * kNB; ++i) expo(S, i);
+    float r[2 * kNB];
 #pragma unroll
-    for (int i = 2; i < 8; ++i) {
-      r0 += s0[i];
-      r1 += s0[8 + i];
-      r2 += s1[i];
-      r3 += s1[8 + i];
+    for (int h = 0; h < 2 * kNB; ++h) {
+      const f32x16& v = S.b[h / 2];
+      const int o8 = 8 * (h & 1);
+      r[h] = v[o8] + v[o8 + 1];
     }
-    l += (r0 + r1) + (r2 + r3);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f32x16& sv = t < 2 ? s0 : s1;
+    for (int i = 2; i < 8; ++i)
+#pragma unroll
+      for (int h = 0; h < 2 * kNB; ++h) r[h] += S.b[h / 2][8 * (h & 1) + i];
+#pragma unroll
+    for (int w = 2 * kNB; w > 1; w /= 2)
+#pragma unroll
+      for (int h = 0; h < w / 2; ++h) r[h] = r[2 * h] + r[2 * h + 1];
+    l += r[0];
+#pragma unroll
+    for (int t = 0; t < kKS; ++t) {
+      f32x16& sv = S.b[t / 2];
       const int r0 = 8 * (t & 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sv[r0 + e] = __uint_as_float(pack2<BF16>(sv[r0 + 2 * e], sv[r0 + 2 * e + 1]));
     }
   }
   // Pins the 16-bit P pairs and l (vec2's results).
-  G9_DEV void pin_p(f32x16& s0, f32x16& s1) {
+  G9_DEV void pin_p(Sc& S) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float a = s0[e], b = s0[8 + e], c = s1[e], d = s1[8 + e];
-      pin(a), pin(b), pin(c), pin(d);
-      s0[e] = a, s0[8 + e] = b, s1[e] = c, s1[8 + e] = d;
-    }
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int blk = 0; blk < kNB; ++blk) {
+        float a = S.b[blk][e], b = S.b[blk][8 + e];
+        pin(a), pin(b);
+        S.b[blk][e] = a, S.b[blk][8 + e] = b;
+      }
     pin(l);
+  }
+  G9_DEV void pin_sc(Sc& S) {
+#pragma unroll
+    for (int blk = 0; blk < kNB; ++blk) pin_vec(S.b[blk]);
   }
   // The eager rescale (every tile) at head dim 128 splits O: the first kSplit
   // head-dim blocks are rescaled in the next dot cluster, as VALU work beside
@@ -380,60 +445,84 @@ struct Pipe {
     for (int d = 0; d < kSplit; ++d) o[d] *= alpha;
   }
 
-  // Interleave of a dot cluster (kNC MFMAs): MFMA i followed by VN VALU
-  // instructions (twice as many at head dim 64, whose clusters have half the
-  // MFMAs for the same softmax work).
-  // An MFMA 32x32x16 takes 32 cycles; about six plain VALU instructions or
-  // two to three exponentials issue beside it without delaying the next one
-  // (measured).
-  template <int VN>
+  // Interleave of a dot cluster (kNF MFMAs): MFMA i followed by VN VALU
+  // instructions and exps_in_slot() exponentials.  An MFMA 32x32x16 takes 32
+  // cycles; about six plain VALU instructions or two to three exponentials
+  // issue beside it without delaying the next one (measured).  Exponentials
+  // are not in the VALU class of sched_group_barrier; left to the scheduler
+  // they bunch up (5-8 in one MFMA slot, none in the next ten), so each slot
+  // gets its own count.  D1 (W = 1) finishes tile j's exponentials, which its
+  // row sums and 16-bit conversions consume later in the same cluster, so
+  // they go early; D2 (W = 2) starts tile j+1's, which nothing in D2 reads,
+  // so they are spread out.  The counts were chosen by measurement (loop
+  // cycles at B=32 S=8192 bf16: head dim 128 v4 -3.4%, v3 +-0; head dim 64
+  // -3.8% and -3.0% against the spread the scheduler picks; the sum over a
+  // cluster is the exponentials it holds: 10 and 22 of 32 at head dim 128,
+  // 20 and 44 of 64 at 64).
+  static constexpr int kEp1[16] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1};  // D1, lazy rescale
+  static constexpr int kEp1e[16] = {4, 3, 3};  // D1 beside the eager rescale's 6 VALU per slot
+  static constexpr int kEp2[16] = {1, 1, 2, 2, 2, 2, 2, 2, 2, 2, 2, 2};
+  static constexpr int kEp1_64[16] = {1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2, 2};
+  static constexpr int kEp2_64[16] = {2, 3, 3, 3, 3, 3, 3, 3, 3, 3, 3, 3, 3, 3, 3};
+  template <int W, int I>
+  G9_DEV static constexpr int exps_in_slot() {
+    if constexpr (HD == 128)
+      return W == 1 ? (LAZY ? kEp1[I] : kEp1e[I]) : kEp2[I];
+    else
+      return W == 1 ? kEp1_64[I] : kEp2_64[I];
+  }
+  static_assert(HD != 128 || sum16(kEp1) == 32 - kE1, "D1 exponentials per slot: re-chosen with the D1/D2 split");
+  static_assert(HD != 128 || sum16(kEp1e) == 32 - kE1, "D1 exponentials per slot: re-chosen with the D1/D2 split");
+  static_assert(HD != 128 || sum16(kEp2) == kE1, "D2 exponentials per slot: re-chosen with the D1/D2 split");
+  static_assert(HD == 128 || sum16(kEp1_64) == 64 - kE1, "D1 exponentials per slot: re-chosen with the D1/D2 split");
+  static_assert(HD == 128 || sum16(kEp2_64) == kE1, "D2 exponentials per slot: re-chosen with the D1/D2 split");
+  template <int VN, int W, int I = 0>
   G9_DEV static void interleave() {
-#pragma unroll
-    for (int i = 0; i < kNC; ++i) {
+    if constexpr (I < kNF) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_VALU, VN * 16 / kNC, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VALU, VN, 0);
+      constexpr int e = exps_in_slot<W, I>();
+      if constexpr (e > 0) __builtin_amdgcn_sched_group_barrier(SG_TRANS, e, 0);
+      interleave<VN, W, I + 1>();
     }
   }
 
-  // One loop iteration; PAR = j & 1 fixes the LDS buffers; (c0, c1) hold
-  // tile j's scores after vec1, (n0, n1) receive tile j+1's; NEXT: tile j+1
-  // exists.  The loop runs over an even number of tiles nte: when nt is odd
-  // the last tile is a phantom past the end of the sequence (its DMAs read
-  // zeros from the buffer range check) whose scores are set to -inf, so it
-  // adds nothing.  Registers are written unconditionally (a read past the
-  // last tile reads a stale but in-bounds buffer), so no value has to survive
-  // a skipped branch.
+  // One loop iteration; PAR = j & 1 fixes the LDS buffers; c holds tile j's
+  // scores after vec1, n receives tile j+1's; NEXT: tile j+1 exists.  The
+  // loop runs over an even number of tiles nte: when nt is odd the last tile
+  // is a phantom past the end of the sequence (its DMAs read zeros from the
+  // buffer range check) whose scores are set to -inf, so it adds nothing.
+  // Registers are written unconditionally (a read past the last tile reads a
+  // stale but in-bounds buffer), so no value has to survive a skipped branch.
   template <int PAR, bool NEXT>
-  G9_DEV void step(int j, f32x16& c0, f32x16& c1, f32x16& n0, f32x16& n1) {
+  G9_DEV void step(int j, Sc& c, Sc& n) {
     // D1(j)
     __builtin_amdgcn_s_setprio(0);
     if constexpr (NEXT) {
-      qk(n0, n1);
-      vec2(c0, c1);
+      qk(n);
+      vec2(c);
       rescale_early();
-      interleave<(kSplit ? G9_FMHA_VN1_EAGER : G9_FMHA_VN1)>();
-      pin_vec(n0);
-      pin_vec(n1);
+      interleave<(kSplit ? G9_FMHA_VN1_EAGER : kVN1), 1>();
+      pin_sc(n);
     } else {
-      vec2(c0, c1);
+      vec2(c);
       rescale_early();
     }
 #pragma unroll
     for (int d = 0; d < kSplit; ++d) pin_vec(o[d]);
-    pin_p(c0, c1);
+    pin_p(c);
     barrier();
     // M1(j): V_j was waited for at the end of M2(j-1) (or the prologue).
     __builtin_amdgcn_s_setprio(1);
     read_v<PAR>();
-    if (j + 2 < nte) waitcnt<kCW, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
+    if (j + 2 < nte) waitcnt<kDW, 15>();  // K_{j+2} landed (V_{j+1} may be in flight)
     if (j + 3 < nte) dma_k(j + 3, PAR ^ 1);
     if constexpr (NEXT) {
-      if (j + 1 >= nt) {  // the phantom tile (a branch, not 32 selects per step)
+      if (j + 1 >= nfull) {  // past the end (a branch, not selects in every step)
         asm volatile("");
-        n0 = f32x16{} - __builtin_inff();
-        n1 = n0;
+        mask(n, p.S - (j + 1) * kBN);
       }
-      vec0(n0, n1);
+      vec0(n);
       pin(m);
       pin(alpha);
     }
@@ -442,13 +531,12 @@ struct Pipe {
     // D2(j)
     __builtin_amdgcn_s_setprio(0);
     if constexpr (NEXT) {
-      pv(c0, c1);
-      vec1(n0, n1);
-      interleave<G9_FMHA_VN2>();
-      pin_vec(n0);
-      pin_vec(n1);
+      pv(c);
+      vec1(n);
+      interleave<kVN2, 2>();
+      pin_sc(n);
     } else {
-      pv(c0, c1);
+      pv(c);
     }
 #pragma unroll
     for (int d = 0; d < kND; ++d) pin_vec(o[d]);
@@ -458,7 +546,7 @@ struct Pipe {
     if constexpr (NEXT) {
       read_k<PAR>();
       if (j + 3 < nte)
-        waitcnt<kCW, 15>();  // V_{j+1} landed (K_{j+3} may be in flight)
+        waitcnt<kDW, 15>();  // V_{j+1} landed (K_{j+3} may be in flight)
       else
         waitcnt<0, 15>();
       rescale();
@@ -486,8 +574,9 @@ G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
 
   PipeT P(p);
   P.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  P.nt = p.S / kBlockN;
+  P.nt = (p.S + PipeT::kBN - 1) / PipeT::kBN;
   P.nte = (P.nt + 1) & ~1;
+  P.nfull = p.S / PipeT::kBN;
   P.lds0 = (u32)(uintptr_t)to_lds(smem);
   const int nte = P.nte, wave = P.wave;
   const char* qb = p.q + b * p.q_b + hq * p.q_h;
@@ -501,10 +590,11 @@ G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
     P.qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (u32)qrow * p.ldq + (16 * s + 8 * h) * 2, 0, 0));
   P.voffk = (u32)lane * p.ldk;
   P.voffv = (u32)lane * p.ldv;
-  P.ak = P.lds0 + h * kPitchK + (lane & 31) * 16;
+  P.ak = P.lds0 + h * PipeT::kPitchK + (lane & 31) * 16;
   {
     const int G = lane >> 4, jj = lane & 15;
-    P.av = P.lds0 + PipeT::kLdsV + (2 * (G & 1) + ((jj & 3) >> 1)) * kPitchV + (4 * (G >> 1) + (jj >> 2)) * 16 + 8 * (jj & 1);
+    P.av = P.lds0 + PipeT::kLdsV + (2 * (G & 1) + ((jj & 3) >> 1)) * PipeT::kPitchV + (4 * (G >> 1) + (jj >> 2)) * 16 +
+           8 * (jj & 1);
   }
   // Prologue: K_0, V_0, K_1 in; S_0 and its first softmax half; K_2 and V_1
   // requested (in that order: the loop expects K_{j+2} before V_{j+1}); K_1
@@ -530,14 +620,15 @@ G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
   waitcnt<0, 15>();
   barrier();
   P.template read_k<0>();
-  f32x16 sa0, sa1, sb0, sb1;
-  P.qk(sa0, sa1);
+  typename PipeT::Sc sa, sb;
+  P.qk(sa);
   waitcnt<63, 0>();
   barrier();  // every wave has read K_0: its buffer takes K_2
   if (nte > 2) P.dma_k(2, 0);
   P.dma_v(1, 1);
-  P.vec0(sa0, sa1);
-  P.vec1(sa0, sa1);
+  if (p.S < PipeT::kBN) P.mask(sa, p.S);  // tile 0 itself ends early
+  P.vec0(sa);
+  P.vec1(sa);
   P.l *= P.alpha;
   P.template read_k<1>();
   waitcnt<63, 0>();
@@ -547,11 +638,11 @@ G9_DEV void fmha_fwd(const FaParams& p, char* smem) {
   if (lag) barrier();
   int j = 0;
   for (; j + 2 < nte; j += 2) {
-    P.template step<0, true>(j, sa0, sa1, sb0, sb1);
-    P.template step<1, true>(j + 1, sb0, sb1, sa0, sa1);
+    P.template step<0, true>(j, sa, sb);
+    P.template step<1, true>(j + 1, sb, sa);
   }
-  P.template step<0, true>(j, sa0, sa1, sb0, sb1);
-  P.template step<1, false>(j + 1, sb0, sb1, sa0, sa1);
+  P.template step<0, true>(j, sa, sb);
+  P.template step<1, false>(j + 1, sb, sa);
   __builtin_amdgcn_s_setprio(0);
   if (!lag) barrier();
   stamp(2);
@@ -606,7 +697,7 @@ extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o,
   if (dtype != G9_F16 && dtype != G9_BF16) return G9_ERR_DTYPE;
   if (variant != 3 && variant != 4) return G9_ERR_SCHEDULE;
   if (B <= 0 || HQ <= 0 || HK <= 0 || S <= 0 || HQ % HK != 0) return G9_ERR_SHAPE;
-  if ((D != 128 && D != 64) || S % fa::kBlockN != 0) return G9_ERR_SHAPE;
+  if ((D != 128 && D != 64) || S % 64 != 0) return G9_ERR_SHAPE;
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return G9_ERR_LAYOUT;
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* ptr[4] = {q, k, v, o};

@@ -186,8 +186,8 @@ def measure(dtype: str, M: int, N: int, K: int, waves: int, settle_s: float = 0.
 def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s: float = 0.8, D: int = 128) -> dict:
     """Phase statistics of one flash-attention launch (g9_fmha_fwd, bhsd,
     head dim D = 128 or 64) at steady state, as ``measure``.  The loop covers
-    all key tiles of 64 (an even count); each costs 2048 * D / 128 ideal MFMA
-    cycles per SIMD (2 waves x D / 4 MFMAs 32x32x16 x 32 cycles)."""
+    all key tiles of 8192 / D keys (64 or 128; an even count); each costs 2048
+    ideal MFMA cycles per SIMD (2 waves x 32 MFMAs 32x32x16 x 32 cycles)."""
     import ctypes
     import time
 
@@ -227,8 +227,8 @@ def measure_fmha(dtype: str, B: int, H: int, S: int, variant: int = 4, settle_s:
     n = min(wgs, lib.g9_timing_capacity())
     buf = np.zeros(n * 8, dtype=np.uint64)
     _lib.check(lib.g9_fmha_timing_read(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "g9_fmha_timing_read")
-    tiles = (S // 64 + 1) // 2 * 2
-    out = phase_stats(buf, tiles, CYCLES_PER_STAGE * D // 128)
+    tiles = (-(-S // (8192 // D)) + 1) // 2 * 2
+    out = phase_stats(buf, tiles, CYCLES_PER_STAGE)
     out.update({"kernel": f"fmha_v{variant}", "dtype": dtype, "B": B, "H": H, "S": S, "D": D,
                 "launch_us": round(launch_us, 2), "tflops": round(compute_flops(B, H, S, S, D, False) / launch_us / 1e6, 1)})
     return out
