@@ -52,6 +52,10 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 # numbers (bf16, kernels/attention/README.md:619-632; no fp16 figure).
 FMHA_SHAPE = {"B": 32, "H": 8, "S": 8192, "D": 128}
 FMHA_REFERENCE_TFLOPS = {("bf16", 4): 1261.0, ("bf16", 3): 1189.0}
+# The reference attention bench's defaults and sequence-length sweep
+# (kernels/attention/bench.py:100, :107-113): B=1, HQ=HK=64, bhsd, bf16.
+FMHA_SWEEP_SEQLENS = (1024, 2048, 4096, 8192, 16384)
+FMHA_SWEEP_SHAPE = {"B": 1, "H": 64}
 
 
 def parse_args():
@@ -79,6 +83,9 @@ def parse_args():
     p.add_argument("--fmha-only", type=int, default=0,
                    help="time only the flash-attention forward (--steps / --warmup / --settle-ms launches of each "
                         "case) and print its object (for profilers)")
+    p.add_argument("--fmha-sweep", type=int, default=0,
+                   help="time only the flash-attention forward over the reference bench's sequence-length sweep "
+                        "(B=1, HQ=HK=64, bf16, head dims 128 and 64, v4 and v3) and print its object")
     p.add_argument("--energy", type=float, default=0.0,
                    help="energy per launch instead: ours vs hipBLASLt for fp16 and bf16, this many seconds of "
                         "back-to-back launches per side and round (two interleaved rounds), amd-smi power sampled")
@@ -618,6 +625,46 @@ def fmha_bench(args, dev) -> dict:
     return out
 
 
+def fmha_sweep(args, dev) -> dict:
+    """The reference attention bench's sequence-length sweep (B=1, HQ=HK=64,
+    bhsd, non-causal, bf16) for head dims 128 and 64, fmha_v4 and fmha_v3:
+    HIP-event time of back-to-back launches over enough rotating (q, k, v, o)
+    sets to exceed 512 MiB, as the reference's rotating_set_count does
+    (kernels/attention/bench.py:186-199)."""
+    import torch
+
+    from gfx950_gluon_tutorials_amd.attention import MetaData, compute_flops, fmha_v3, fmha_v4
+
+    B, H = FMHA_SWEEP_SHAPE["B"], FMHA_SWEEP_SHAPE["H"]
+    out = {}
+    for D in (128, 64):
+        for S in FMHA_SWEEP_SEQLENS:
+            per_set = 4 * B * H * S * D * 2
+            nsets = max(1, -(-(512 << 20) // per_set))
+            g = torch.Generator(device=dev).manual_seed(S + D)
+            sets = []
+            for _ in range(nsets):
+                q, k, v = (torch.randn(B, H, S, D, device=dev, dtype=torch.bfloat16, generator=g) for _ in range(3))
+                sets.append((q, k, v, torch.empty_like(q)))
+            md = MetaData(sm_scale=D**-0.5)
+            md.max_seqlens_q = md.max_seqlens_k = S
+            md.layout = "bhsd"
+            flop = compute_flops(B, H, S, S, D, False)
+            for variant, fn in ((4, fmha_v4.run_gluon_attention), (3, fmha_v3.run_gluon_attention)):
+                def launch(i, schedule="dp", fn=fn):
+                    fn(*sets[i % nsets], md)
+
+                ms = time_case(launch, args.steps, args.warmup, settle_s=args.settle_ms / 1e3)
+                tf = flop / (ms * 1e-3) / 1e12
+                out[f"d{D}_s{S}_v{variant}"] = {"tflops": round(tf, 2), "ms": round(ms, 5), "sets": nsets}
+                print(f"# fmha_v{variant} bf16 B={B} H={H} S={S} D={D}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS "
+                      f"({nsets} set(s))", flush=True)
+            del sets
+            torch.cuda.empty_cache()
+    out["shape"] = dict(FMHA_SWEEP_SHAPE, layout="bhsd", causal=False, dtype="bf16")
+    return out
+
+
 def energy_study(args, dev) -> dict:
     """Energy per 4096x4096x8192 launch of our 4-wave data-parallel kernel and
     of hipBLASLt's (torch.matmul) for fp16 and bf16, on one box: each side runs
@@ -700,6 +747,9 @@ def main():
         return
     if args.fmha_only:
         print(json.dumps({"fmha": fmha_bench(args, dev)}), flush=True)
+        return
+    if args.fmha_sweep:
+        print(json.dumps({"fmha_sweep": fmha_sweep(args, dev)}), flush=True)
         return
     if args.energy:
         print(json.dumps({"energy": energy_study(args, dev)}), flush=True)

@@ -217,6 +217,34 @@ def test_benchmark_shape_on_sampled_rows(gpu, dtype):
         assert abs(got_l[b, h, s] - ref_l[0]) <= 2 * A.FINFO_EPS[DT_NAME[DT[dtype]]] * bound + 1e-4
 
 
+@pytest.mark.parametrize("D,variant", [(128, 4), (64, 3)])
+def test_longest_sweep_shape_on_sampled_rows(gpu, D, variant):
+    # The longest point of the reference bench's sweep (B=1, HQ=HK=64,
+    # S=16384, kernels/attention/bench.py:100,107-113): 256 key tiles at head
+    # dim 128, 128 at 64; 40 sampled rows against the oracle.
+    B, H, S = 1, 64, 16384
+    torch.manual_seed(17 + D)
+    q, k, v = (torch.randn(B, H, S, D, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    md = MetaData(sm_scale=D**-0.5)
+    md.max_seqlens_q = md.max_seqlens_k = S
+    md.layout = "bhsd"
+    o = torch.empty_like(q)
+    (fmha_v4 if variant == 4 else fmha_v3).run_gluon_attention(q, k, v, o, md)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    rng = np.random.default_rng(18 + D)
+    rows = [(0, int(rng.integers(H)), int(rng.integers(S))) for _ in range(36)]
+    rows += [(0, 0, 0), (0, H - 1, S - 1), (0, 7, 8191), (0, 7, 8192)]
+    heads = sorted({(b, h) for b, h, _ in rows})
+    cpu = {(b, h): [t[b, h].float().cpu().numpy() for t in (q, k, v)] for b, h in heads}
+    got = o.float().cpu().numpy()
+    for b, h, s in rows:
+        qq, kk, vv = cpu[(b, h)]
+        ref, _ = A.sdpa_rows(qq[None, None], kk[None, None], vv[None, None], [(0, 0, s)], md.sm_scale)
+        ok, mx, _ = A.within_tolerance(got[b, h, s][None], ref, "bfloat16")
+        assert ok, f"row {(b, h, s)}: max |diff| {mx:.3g}"
+
+
 @pytest.mark.parametrize("variant", [3, 4])
 def test_nan_inputs_give_nan_rows(gpu, variant):
     # As the reference's fp32 SDPA: a NaN in a query row makes that row NaN; a
