@@ -212,6 +212,13 @@ G9_DEV u32x2 tr_read(u32 addr) {
 #define G9_FMHA_VEC1_EXPS_64 44  // head dim 64: exponentials of a tile (of 64 per lane) done in D2
 #endif
 
+// Sum of a 16-entry table (compile time).
+constexpr int sum16(const int (&a)[16]) {
+  int t = 0;
+  for (int i = 0; i < 16; ++i) t += a[i];
+  return t;
+}
+
 // SOQ: the scale is folded into Q, so the scores already are in log2 units
 // and the exponent argument is a 2-source subtract instead of a 3-source fma
 // (fewer register-file reads beside the other wave's LDS returns).
@@ -220,12 +227,6 @@ G9_DEV u32x2 tr_read(u32 addr) {
 // so a dot cluster holds 16 MFMAs either way and the two head dims share the
 // per-cluster costs (barriers, the row-max chain, waits) over the same MFMA
 // work.  A tile's scores are kNB blocks of 32 keys (Sc).
-constexpr int sum16(const int (&a)[16]) {
-  int t = 0;
-  for (int i = 0; i < 16; ++i) t += a[i];
-  return t;
-}
-
 template <bool BF16, bool LAZY, bool SOQ, int HD>
 struct Pipe {
   static_assert(HD == 64 || HD == 128, "head dim 64 or 128");
