@@ -129,12 +129,10 @@ G9_DEV float xhalf(float x, F op) {
 // it adds no wait for these DMAs before LDS reads (it cannot tell the read
 // addresses from the DMA targets apart and would wait for every DMA in
 // flight).  The caller orders them with explicit vmcnt waits and barriers.
-// M0 is written here; nothing else in these kernels uses it.
+// The LDS address goes in through an M0 operand, so the compiler writes M0
+// itself and knows what it holds.
 G9_DEV void dma16_untracked(rsrc_t r, u32 lds, u32 voff, u32 soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds), "v"(voff), "s"(r), "s"(soff)
-               : "memory");
+  asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" : : "{m0}"(lds), "v"(voff), "s"(r), "s"(soff) : "memory");
 }
 
 // Pins a value to this point of the program: the compiler can neither move
@@ -717,7 +715,11 @@ extern "C" int g9_fmha_fwd(const void* q, const void* k, const void* v, void* o,
   if (lse && (uintptr_t)lse % 4 != 0) return G9_ERR_LAYOUT;
   const int64_t mblocks = (S + fa::kBlockM - 1) / fa::kBlockM;
   if (B * HQ * mblocks > INT32_MAX) return G9_ERR_SHAPE;
-  if (!(sm_scale > 0.f)) return G9_ERR_SHAPE;
+  // This file is compiled without NaN semantics (-fno-honor-nans), under
+  // which a float comparison may treat NaN as ordered: the scale's bits are
+  // tested instead (a positive, finite, nonzero float).
+  const u32 sm_bits = __builtin_bit_cast(u32, sm_scale);
+  if ((sm_bits >> 31) != 0 || sm_bits == 0 || ((sm_bits >> 23) & 0xff) == 0xff) return G9_ERR_SHAPE;
   fa::FaParams p{};
   p.q = static_cast<const char*>(q);
   p.k = static_cast<const char*>(k);

@@ -222,6 +222,10 @@ def _call(**kw):
     (dict(HQ=3, HK=2), _lib.G9_ERR_SHAPE),
     (dict(scale=0.0), _lib.G9_ERR_SHAPE),
     (dict(scale=float("nan")), _lib.G9_ERR_SHAPE),
+    (dict(scale=-float("nan")), _lib.G9_ERR_SHAPE),
+    (dict(scale=float("inf")), _lib.G9_ERR_SHAPE),
+    (dict(scale=-0.088), _lib.G9_ERR_SHAPE),
+    (dict(scale=-0.0), _lib.G9_ERR_SHAPE),
     (dict(q=0), _lib.G9_ERR_LAYOUT),
     (dict(v=FAKE + 2), _lib.G9_ERR_LAYOUT),
     (dict(qs=(2 * 128 * 128, 128 * 128, 128, 2)), _lib.G9_ERR_LAYOUT),
