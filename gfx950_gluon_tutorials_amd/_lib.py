@@ -34,6 +34,7 @@ G9_BF16 = 1
 G9_BF8 = 2
 G9_FP4 = 3
 G9_FP4P = 4  # MXFP4 with preshuffled scales (g9_gemm_a4w4_preshuffled)
+G9_FP4K = 5  # MXFP4 with K-major scales (g9_gemm_a4w4 given K-major scale views)
 
 # Schedules.
 G9_SCHED_DP = 0
@@ -71,6 +72,9 @@ SIGNATURES = {
     "g9_workspace_size": (_sz, [_int, _i64, _i64, _i64, _int, _int]),
     "g9_workspace_init": (_int, [_vp, _sz, _vp]),
     "g9_workspace_error": (_int, [_vp, _sz, _vp, ctypes.POINTER(_int)]),
+    "g9_workspace_watch": (_int, [_vp, _sz, _vp, _vp]),
+    "g9_set_streamk_spin_limit": (ctypes.c_uint32, [ctypes.c_uint32]),
+    "g9_noalloc_error": (_int, [_vp, ctypes.POINTER(_int)]),
     "g9_kernel_name": (ctypes.c_char_p, [_int, _int, _int, _int]),
     "g9_status_string": (ctypes.c_char_p, [_int]),
     "g9_streamk_workgroups": (_int, []),

@@ -47,6 +47,23 @@ extern "C" __global__ G9_ATTRS(G9Fp4p4) void g9_a4w4ps_f16out_dp_4w(GemmParams p
   gemm_dp<Op::FP4P, OUT_F16, G9Fp4p4>(p);
 }
 
+// MXFP4 with K-major scales (the reference bench's transposed scale views):
+// 4-wave, data-parallel, stream-K and split-K.
+using G9Fp4k4 = Geo4<kMfmaDim<Op::FP4K>>;
+extern "C" __global__ G9_ATTRS(G9Fp4k4) void g9_a4w4km_bf16out_dp_4w(GemmParams p) {
+  gemm_dp<Op::FP4K, OUT_BF16, G9Fp4k4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Fp4k4) void g9_a4w4km_f16out_dp_4w(GemmParams p) {
+  gemm_dp<Op::FP4K, OUT_F16, G9Fp4k4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Fp4k4) void g9_a4w4km_bf16out_sk_4w(GemmParams p) {
+  gemm_sk<Op::FP4K, OUT_BF16, G9Fp4k4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Fp4k4) void g9_a4w4km_f16out_sk_4w(GemmParams p) {
+  gemm_sk<Op::FP4K, OUT_F16, G9Fp4k4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Fp4k4) void g9_a4w4km_splitk_4w(GemmParams p) { gemm_splitk<Op::FP4K, G9Fp4k4>(p); }
+
 // Grouped (MoE) kernels, 4-wave.
 #define G9_DEFINE_MOE(NAME, OP, OUT)                                                                \
   extern "C" __global__ G9_ATTRS(NAME##_g4) void NAME##_moe_4w(GemmParams p) {                      \
@@ -101,6 +118,10 @@ const KernelEntry kKernels[] = {
     G9_ENTRY(G9_FP4, G9_BF16, g9_a4w4_bf16out),  G9_ENTRY(G9_FP4, G9_F16, g9_a4w4_f16out),
     {G9_FP4P, G9_BF16, G9_SCHED_DP, 4, g9_a4w4ps_bf16out_dp_4w, "g9_a4w4ps_bf16out_dp_4w"},
     {G9_FP4P, G9_F16, G9_SCHED_DP, 4, g9_a4w4ps_f16out_dp_4w, "g9_a4w4ps_f16out_dp_4w"},
+    {G9_FP4K, G9_BF16, G9_SCHED_DP, 4, g9_a4w4km_bf16out_dp_4w, "g9_a4w4km_bf16out_dp_4w"},
+    {G9_FP4K, G9_F16, G9_SCHED_DP, 4, g9_a4w4km_f16out_dp_4w, "g9_a4w4km_f16out_dp_4w"},
+    {G9_FP4K, G9_BF16, G9_SCHED_SK, 4, g9_a4w4km_bf16out_sk_4w, "g9_a4w4km_bf16out_sk_4w"},
+    {G9_FP4K, G9_F16, G9_SCHED_SK, 4, g9_a4w4km_f16out_sk_4w, "g9_a4w4km_f16out_sk_4w"},
 };
 
 #define G9_SPLITK_ENTRY(DT, OUT, NAME)                                                              \
@@ -112,6 +133,8 @@ const KernelEntry kSplitKernels[] = {
     G9_SPLITK_ENTRY(G9_F16, G9_F16, g9_a16w16_f16),  G9_SPLITK_ENTRY(G9_BF16, G9_BF16, g9_a16w16_bf16),
     G9_SPLITK_ENTRY(G9_BF8, G9_F16, g9_a8w8),        G9_SPLITK_ENTRY(G9_BF8, G9_BF16, g9_a8w8),
     G9_SPLITK_ENTRY(G9_FP4, G9_BF16, g9_a4w4),       G9_SPLITK_ENTRY(G9_FP4, G9_F16, g9_a4w4),
+    {G9_FP4K, G9_BF16, G9_SCHED_SPLITK, 4, g9_a4w4km_splitk_4w, "g9_a4w4km_splitk_4w"},
+    {G9_FP4K, G9_F16, G9_SCHED_SPLITK, 4, g9_a4w4km_splitk_4w, "g9_a4w4km_splitk_4w"},
 };
 
 const KernelEntry kMoeKernels[] = {
@@ -147,6 +170,7 @@ int stage_k(int dtype) {
       return 128;
     case G9_FP4:
     case G9_FP4P:
+    case G9_FP4K:
       return 256;
   }
   return 0;
@@ -162,6 +186,11 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 size_t flags_bytes(long long tiles) { return align256((size_t)tiles * 4); }
 
 std::atomic<unsigned> g_epoch{0};
+
+// Polls of a stream-K flag wait before it gives up and sets the workspace
+// error word (g9_set_streamk_spin_limit changes it, for tests of that path).
+constexpr uint32_t kDefaultSpinLimit = 1u << 26;
+std::atomic<uint32_t> g_spin_limit{kDefaultSpinLimit};
 
 // CUs of the current device (cached per device; 0 if it cannot be queried).
 int cu_count() {
@@ -247,6 +276,7 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     p.flags = reinterpret_cast<u32*>(w + kWsHeader);
     p.ws = reinterpret_cast<float*>(w + base);
     p.epoch = (g_epoch.fetch_add(1) % 65535u) + 1u;
+    p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
     const long long units = tiles * p.ns;
     int cus = cu_count();
     if (cus <= 0) return G9_ERR_HIP;
@@ -402,10 +432,27 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
   if ((st = check_operand(a, stride_am, stride_ak, K / 2))) return st;
   if ((st = check_operand(b, stride_bn, stride_bk, K / 2))) return st;
   if (!a_scales || !b_scales) return G9_ERR_LAYOUT;
-  if (stride_ask != 1 || stride_bsk != 1) return G9_ERR_LAYOUT;
   if (!aligned(a_scales, 4) || !aligned(b_scales, 4)) return G9_ERR_LAYOUT;
-  if (stride_asm % 4 || stride_bsn % 4 || stride_asm < K / 32 || stride_bsn < K / 32) return G9_ERR_LAYOUT;
-  if (stride_asm > (1 << 24) || stride_bsn > (1 << 24)) return G9_ERR_LAYOUT;
+  // Row-major scales (K/32 contiguous groups per row), or K-major for both
+  // operands (rows contiguous, groups stride_ask / stride_bsk bytes apart:
+  // the transposed views the reference bench passes), which the 4-wave
+  // kernels read without a re-layout.
+  const bool kmajor = stride_asm == 1 && stride_bsn == 1 && stride_ask != 1 && stride_bsk != 1;
+  int dtype = G9_FP4;
+  if (kmajor) {
+    if (waves != 4) return G9_ERR_SCHEDULE;
+    if (stride_ask % 4 || stride_bsk % 4 || stride_ask < M || stride_bsk < N) return G9_ERR_LAYOUT;
+    // Group offsets stay below the kernels' 2^31 dead offset.
+    if ((K / 32) * stride_ask + 4096 >= (int64_t(1) << 31) || (K / 32) * stride_bsk + 4096 >= (int64_t(1) << 31))
+      return G9_ERR_SHAPE;
+    dtype = G9_FP4K;
+    stride_asm = stride_ask;
+    stride_bsn = stride_bsk;
+  } else {
+    if (stride_ask != 1 || stride_bsk != 1) return G9_ERR_LAYOUT;
+    if (stride_asm % 4 || stride_bsn % 4 || stride_asm < K / 32 || stride_bsn < K / 32) return G9_ERR_LAYOUT;
+    if (stride_asm > (1 << 24) || stride_bsn > (1 << 24)) return G9_ERR_LAYOUT;
+  }
   GemmParams p{};
   p.a = static_cast<const char*>(a);
   p.b = static_cast<const char*>(b);
@@ -417,11 +464,11 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
   p.K = (int)K;
   p.lda = (u32)stride_am;
   p.ldb = (u32)stride_bn;
-  p.ldsa = (u32)stride_asm;
+  p.ldsa = (u32)stride_asm;  // K-major: bytes between scale groups
   p.ldsb = (u32)stride_bsn;
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(G9_FP4));
-  return launch(G9_FP4, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+  return launch(dtype, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
 }
 
 int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
@@ -595,6 +642,12 @@ __global__ void zero_words(u32* p, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
 }
+__global__ void set_words2(u32* p, u32 lo, u32 hi) {
+  if (threadIdx.x == 0) {
+    p[0] = lo;
+    p[1] = hi;
+  }
+}
 }  // namespace
 
 extern "C" {
@@ -616,6 +669,25 @@ int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
                  hipSuccess
              ? G9_OK
              : G9_ERR_HIP;
+}
+
+int g9_workspace_watch(void* workspace, size_t workspace_bytes, int* host_flag, void* stream) {
+  if (!workspace || workspace_bytes < kWsHeader || !aligned(workspace, 256)) return G9_ERR_WORKSPACE;
+  if (host_flag && !aligned(host_flag, 4)) return G9_ERR_LAYOUT;
+  // Header bytes 8-15 hold the flag's address; written by a kernel on the
+  // stream (no memset or copy, so the call can be captured in a graph).
+  u32* w = reinterpret_cast<u32*>(static_cast<char*>(workspace) + 8);
+  const uint64_t a = reinterpret_cast<uintptr_t>(host_flag);
+  u32 lo = (u32)a, hi = (u32)(a >> 32);
+  void* args[] = {&w, &lo, &hi};
+  return hipLaunchKernel(reinterpret_cast<const void*>(set_words2), dim3(1), dim3(64), args, 0,
+                         reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}
+
+uint32_t g9_set_streamk_spin_limit(uint32_t polls) {
+  return g_spin_limit.exchange(polls ? polls : kDefaultSpinLimit);
 }
 
 int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stream, int* error) {
@@ -733,6 +805,19 @@ int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int
   // Split-K writes every partial it reads, so it needs no clearing.
   if (schedule == G9_SCHED_SK && (st = g9_workspace_init(ws, kScratchBytes, stream))) return st;
   return launch(dtype, dtype, schedule, waves, p, ws, kScratchBytes, stream);
+}
+
+int g9_noalloc_error(void* stream, int* error) {
+  if (!error) return G9_ERR_LAYOUT;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int dev = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess) return G9_ERR_HIP;
+  DeviceGuard guard(dev);
+  if (!guard.ok) return G9_ERR_HIP;
+  void* ws = nullptr;
+  const int st = scratch_ptr(dev, &ws);
+  if (st) return st;
+  return g9_workspace_error(ws, kScratchBytes, stream, error);
 }
 
 int g9_version(void) { return 100; }

@@ -113,10 +113,18 @@ G9_DEV void sk_stamp(int) {}
 G9_DEV void sk_times_store(const SkTimes&) {}
 #endif
 
-// FP4P: MXFP4 with preshuffled E8M0 scales (see Pipe::init): the same data
-// and MFMAs as FP4, but each lane's scale bytes for four stages arrive with
-// one LDS read and no byte permute.
-enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3, FP4P = 4 };
+// MXFP4 comes with its E8M0 scales in one of three global layouts, all fed
+// to the same MFMAs:
+//   FP4  row-major (M rows of K/32 bytes): each 4-stage scale chunk lands in
+//        LDS as it is in memory and is transposed in place once (see
+//        Pipe::xform_read), after which it has the FP4K layout;
+//   FP4K K-major (K/32 groups of M bytes, the layout of the reference bench's
+//        transposed scale views): the chunk DMA writes the transposed layout
+//        directly;
+//   FP4P preshuffled (quant.preshuffle_e8m0).
+// With 16x16 fragments every layout gives a lane all its scale bytes of a
+// chunk with one LDS read per fragment (ScRegs) and no byte permute.
+enum class Op : int { F16 = 0, BF16 = 1, BF8 = 2, FP4 = 3, FP4P = 4, FP4K = 5 };
 enum : int { OUT_F16 = 0, OUT_BF16 = 1 };
 
 struct GemmParams {
@@ -140,7 +148,9 @@ struct GemmParams {
   float* ws;                  // fp32 partial tiles (256 KiB per tile)
   u32* flags;                 // one flag per tile: (epoch << 16) | stages done
   u32 epoch;
-  int* err;                   // set to 1 when a flag wait times out
+  int* err;                   // set to 1 when a flag wait times out (workspace header; a host
+                              // flag registered at byte 8 of the header is set as well)
+  u32 spin_limit;             // polls of a flag wait before it gives up
   int sk_ctas;                // persistent workgroups
   // split-K: K segments per tile (the partials go to ws)
   int split;
@@ -243,12 +253,13 @@ struct Frag {
 
 template <Op OP>
 struct OpInfo {
-  static constexpr bool kScaled = OP == Op::FP4 || OP == Op::FP4P;
+  static constexpr bool kScaled = OP == Op::FP4 || OP == Op::FP4P || OP == Op::FP4K;
   static constexpr bool kPreshuffled = OP == Op::FP4P;
+  static constexpr bool kKMajor = OP == Op::FP4K;
   static constexpr int kChunksPerMfma = OP == Op::BF8 ? 2 : 1;  // 16-byte chunks per lane per MFMA
 };
 template <Op OP>
-constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : OP == Op::FP4P ? 16 : G9_MD_F16;
+constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 : OP == Op::FP4P || OP == Op::FP4K ? 16 : G9_MD_F16;
 // The 8-wave MXFP4 kernel uses 32x32x64 fragments: with 16x16 ones its
 // operand sets, scale bytes and DMA offsets exceed the 128 VGPRs a wave has
 // beside its accumulators at 2 waves per SIMD, and the spill reloads inside
@@ -258,6 +269,21 @@ constexpr int kMfmaDim = OP == Op::BF8 ? G9_MD_BF8 : OP == Op::FP4 ? G9_MD_FP4 :
 #endif
 template <Op OP>
 constexpr int kMfmaDim8 = OP == Op::FP4 || OP == Op::FP4P ? G9_MD_FP4_8W : kMfmaDim<OP>;
+
+// Scale paths of the scaled kernels:
+//  * kTrScales: chunks in LDS in the transposed ("KM") layout, read with
+//    ds_read_b64_tr_b8 -- FP4 and FP4K with 16x16 fragments and 4 waves;
+//  * kXform: FP4 of those, whose row-major chunks are transposed in place;
+//  * kChunkScales: a lane reads all its scale bytes of a chunk at once into
+//    ScRegs (kTrScales and FP4P).  The other FP4 kernels (8 waves with 32x32
+//    fragments) read one scale word per fragment and stage from row-major
+//    chunks.
+template <Op OP, class G>
+constexpr bool kTrScales = (OP == Op::FP4 || OP == Op::FP4K) && G::MD == 16 && G::NW == 4;
+template <Op OP, class G>
+constexpr bool kXform = OP == Op::FP4 && kTrScales<OP, G>;
+template <Op OP, class G>
+constexpr bool kChunkScales = OP == Op::FP4P || kTrScales<OP, G>;
 
 // Per-region work and the DMA pattern of the main loop.  The loop body covers
 // kBody stages = 4 * kBody regions, numbered by their body position.  Every
@@ -453,9 +479,15 @@ struct Slots {
   static constexpr int kScaleDmaQ = dma_q(D - 1) + 2 < NQ ? dma_q(D - 1) + 2 : NQ - 1;
   static constexpr int kLastQ = (read_q(NR - 1) > scale_q(NF - 1) ? read_q(NR - 1) : scale_q(NF - 1)) + 3;
   static constexpr int perm_q(int F) { return NQ - NF - 1 + F; }
+  // kXform: slot of a region's transpose reads or writes (after the
+  // operand reads, between the operand DMAs).
+#ifndef G9_XFORM_Q
+#define G9_XFORM_Q 17
+#endif
+  static constexpr int kXformQ = G9_XFORM_Q < NQ ? G9_XFORM_Q : NQ - 1;
   static_assert(NQ >= 1, "a region needs an MFMA after its barrier");
   static_assert(!OpInfo<OP>::kScaled || scale_q(NF - 1) < NQ, "scale reads must fit the region");
-  static_assert(!OpInfo<OP>::kScaled || OpInfo<OP>::kPreshuffled || G::MD != 16 || perm_q(0) >= kLastQ,
+  static_assert(!OpInfo<OP>::kScaled || kChunkScales<OP, G> || G::MD != 16 || perm_q(0) >= kLastQ,
                 "permutes must follow the scale reads");
 };
 
@@ -479,21 +511,46 @@ G9_DEV u32 opaque_s(u32 x) {
 // traffic) and the sum does not wrap.
 constexpr u32 kDeadOff = 0x80000000u;
 
-// FP4P: a wave's E8M0 scales of one chunk (four stages), one u32x2 per
-// fragment: .x holds stages 0-1 and .y stages 2-3, byte 2 * (stage & 1) + step
-// of each.  A fragment set's scales are read when the region that reads its
-// operands reaches the chunk's first stage.  B0 is used in a stage's first
-// and last regions, so its last use in one chunk and its first in the next
-// are adjacent regions; its registers alternate by chunk parity.  The other
-// sets have two regions between those uses and are overwritten in place.
-template <Op OP, class G>
+// ds_read_b64_tr_b8 at LDS address addr + IMM (see Pipe::init for its lane
+// map), and a 16-byte LDS store.  Both are inline assembly: the compiler
+// cannot tell a transpose read of the scale chunks from the LDS-DMA writes
+// in flight and would put a vmcnt(0) wait before each one (measured in the
+// built code), and the stores that complete a transpose must stay ordered
+// with those reads.  The compiler does not wait for the read's result
+// either: every use comes after a region-start lgkmcnt(0), and isa_check.py
+// proves on the built code that nothing touches the destination earlier.
+template <int IMM>
+G9_DEV u32x2 tr_read(u32 addr) {
+  static_assert(IMM >= 0 && IMM < 65536, "DS offsets are 16 bits");
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(IMM) : "memory");
+  return v;
+}
+template <int IMM>
+G9_DEV void lds_store16(u32 addr, u32x2 lo, u32x2 hi) {
+  static_assert(IMM >= 0 && IMM < 65536, "DS offsets are 16 bits");
+  const u32x4 v = {lo.x, lo.y, hi.x, hi.y};
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "i"(IMM) : "memory");
+}
+
+// kChunkScales: a wave's E8M0 scales of one chunk (four stages), one u32x2
+// per fragment: .x holds stages 0-1 and .y stages 2-3, byte 2 * (stage & 1) +
+// step of each.  A fragment set's scales are read when the region that reads
+// its operands reaches the chunk's first stage.  B0 is used in a stage's
+// first and last regions, so its last use in one chunk and its first in the
+// next are adjacent regions; its registers alternate by chunk parity.  The
+// other sets have two regions between those uses and are overwritten in
+// place.  kXform adds the two transposed units of the part being transposed,
+// held from the region that reads them to the region that writes them back.
+template <Op OP, class G, bool = kChunkScales<OP, G>>
 struct ScRegs {};
-template <class G>
-struct ScRegs<Op::FP4P, G> {
-  static_assert(G::MD == 16, "preshuffled scales are read for 16x16 fragments");
+template <Op OP, class G>
+struct ScRegs<OP, G, true> {
+  static_assert(G::MD == 16, "chunk scales are read for 16x16 fragments");
   u32x2 a[2][G::FM];   // A0, A1
   u32x2 b1[G::FN];
   u32x2 b0[2][G::FN];  // B0, by chunk parity
+  u32x2 t[2];          // kXform
 };
 
 // Per-workgroup pipeline state: buffer resources, per-lane DMA offsets and LDS
@@ -501,6 +558,7 @@ struct ScRegs<Op::FP4P, G> {
 template <Op OP, class G>
 struct Pipe {
   using I = OpInfo<OP>;
+  static_assert(!I::kKMajor || kTrScales<OP, G>, "K-major scales are read by the 4-wave 16x16 kernels");
   static constexpr int D = G::kDmaPerSub;
   static constexpr int SP = I::kScaled ? G::kScParts : 1;
   rsrc_t rA[2], rB[2];      // operand half-tiles
@@ -508,9 +566,12 @@ struct Pipe {
   u32 vA[D], vB[D];         // DMA offsets of the wave's 1-KiB runs
   u32 vS[SP];               // FP4: chunk DMA offsets (32 rows x 32 bytes each)
   u32 bA[G::NC], bB[G::NC];  // LDS read bases of the lane's chunks (A at 0, B at 64 KiB)
-  u32 bS[2][2];             // FP4: LDS read bases [A/B][stages 0-1 / 2-3 of a chunk]
+  u32 bS[2][2];             // FP4: LDS read bases [A/B][stages 0-1 / 2-3 of a chunk] (kTrScales:
+                            // [A/B][fragment parity])
+  u32 tb[2], tw;            // kXform: LDS bases of the transpose's reads and writes
   u32 sel;                  // FP4, MD 16: scale byte selector
-  u32 cstride;              // FP4P: bytes between consecutive scale chunks of this wave's operand
+  u32 cstride;              // FP4P: bytes between consecutive scale chunks of this wave's operand;
+                            // FP4K: bytes between consecutive scale groups
   u32 lds0;                 // LDS address of the shared buffer
   u32 mrow;                 // LDS address of the wave's rows in sub-buffer A0, slot 0
   u32 msc;                  // FP4: LDS address of the wave's chunk rows in chunk slot 0
@@ -603,9 +664,8 @@ struct Pipe {
       sel = 0;
     } else if constexpr (I::kScaled) {
       // The wave loads chunk rows [xw * 128 + r0, + kScRows) of the 512: half
-      // tile xw (0: A0, 1: A1, 2: B0, 3: B1), rows r0.. of it.  Part j covers
-      // 32 of them, two lanes per row; lane l fetches the 16-byte half that
-      // belongs in its LDS half under the bit-3 row swap.
+      // tile xw (0: A0, 1: A1, 2: B0, 3: B1), rows r0.. of it, as kScParts
+      // 1-KiB parts of 32 rows.
       // The resource is built from wave-uniform scalars (a select between
       // prebuilt resources is lowered through VGPRs, which turns every DMA
       // into a per-lane loop).
@@ -615,28 +675,87 @@ struct Pipe {
       const u32 lds = sa ? p.ldsa : p.ldsb;
       const int hrow = (sa ? tm : tn) * kTile + (xw & 1) * 128;
       const int hvalid = __builtin_amdgcn_readfirstlane(min(max((sa ? p.M : p.N) - hrow, 0), 128));
-      const unsigned char* hbase = (sa ? p.a_sc : p.b_sc) + (size_t)hrow * lds;
-      rS = make_rsrc(hbase, (u32)hvalid * lds);
-#pragma unroll
-      for (int j = 0; j < SP; ++j) {
-        const int row = r0 + 32 * j + (lane >> 1);
-        const int half = (lane & 1) ^ ((row >> 3) & 1);
-        vS[j] = (u32)row * lds + half * 16;
-      }
       msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
-      // MD 16 reads the row's 8 scale bytes of a stage and picks groups gi
-      // and 4 + gi (byte 0x0c of a v_perm selector yields zero); MD 32 reads
-      // the dword of groups 4gi..4gi+3 directly.  Fragment rows are multiples
-      // of 16, so the row swap depends on rr only.
-      const u32 word = G::MD == 32 ? 4u * gi : 0u;
-      const int ssw = (rr >> 3) & 1;
+      if constexpr (I::kKMajor) {
+        // K-major scales: group q of the operand at q * lds, rows contiguous.
+        // The chunk's KM layout (below) is written directly: lane l of part
+        // j fills group row l / 2 of the part, i.e. group G = 4 (p & 7) +
+        // (p >> 3) of p = l / 2, with the 16 rows 16 ((l & 1) ^ (G & 1)) ..
+        // of the part.  Rows past the operand's end read the next group's
+        // first rows (scales of A or B rows that read zero, whose outputs are
+        // not stored) or, in the last group, zero.
+        cstride = __builtin_amdgcn_readfirstlane(lds);
+        const u32 groups = (u32)p.K / 32;
+        rS = make_rsrc((sa ? p.a_sc : p.b_sc) + hrow, (groups - 1) * lds + (u32)hvalid);
+        const int pr = lane >> 1, grp = 4 * (pr & 7) + (pr >> 3);
 #pragma unroll
-      for (int g = 0; g < (G::NW == 4 ? 2 : 1); ++g) {
-        bS[0][g] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
-        bS[1][g] =
-            opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
+        for (int j = 0; j < SP; ++j) vS[j] = (u32)grp * lds + (u32)(r0 + 32 * j) + 16u * ((lane & 1) ^ (grp & 1));
+      } else {
+        // Row-major scales: lane l of part j fetches the 16-byte half of row
+        // 32 j + l / 2 that belongs in its LDS half under the bit-3 row swap.
+        const unsigned char* hbase = (sa ? p.a_sc : p.b_sc) + (size_t)hrow * lds;
+        rS = make_rsrc(hbase, (u32)hvalid * lds);
+#pragma unroll
+        for (int j = 0; j < SP; ++j) {
+          const int row = r0 + 32 * j + (lane >> 1);
+          const int half = (lane & 1) ^ ((row >> 3) & 1);
+          vS[j] = (u32)row * lds + half * 16;
+        }
       }
-      sel = (u32)gi | ((u32)(4 + gi) << 8) | 0x0c0c0000u;
+      if constexpr (kTrScales<OP, G>) {
+        // KM layout of a chunk slot: half tile X at X * 4096, its part jj
+        // (rows 32 jj .. 32 jj + 31) at + jj * 1024; in a part, group G
+        // (0..31) is a 32-byte row at position p(G) = (G >> 2) + 8 (G & 3),
+        // holding the part's four 8-row octets, octet o at 8 (o ^ 2 (G & 1)):
+        // the scales of rows 8o .. 8o + 7, in row order.
+        // ds_read_b64_tr_b8 gives lane 8a + b of each 16-lane group byte b of
+        // the 8-byte units addressed by lanes a, a + 2, ..., a + 14 of the
+        // group (measured on gfx950).  Lane 16g + 2k + a addresses the unit
+        // of group 4k + g and octet a of the fragment's two, so lane (g, row
+        // rr) receives the scales of its row for groups g, 4 + g, ..., 28 + g:
+        // byte 2 st + h is stage st, MFMA step h, as the MFMAs take them.
+        // Per 32 lanes (two lane groups) the 16 units sit on 64 distinct
+        // banks.
+        const int g = lane >> 4, k = (lane >> 1) & 7, a = lane & 1;
+#pragma unroll
+        for (int f2 = 0; f2 < 2; ++f2) {
+          const u32 off = 32u * (u32)(k + 8 * g) + 8u * (u32)((2 * f2 + a) ^ (2 * (g & 1)));
+          bS[0][f2] = opaque(lds0 + kScaleBase + (u32)wm * 2048u + off);
+          bS[1][f2] = opaque(lds0 + kScaleBase + 8192u + (u32)wn * 2048u + off);
+        }
+        if constexpr (kXform<OP, G>) {
+          // In-place transpose of a row-major part (32 rows x 32 bytes, the
+          // halves of rows with bit 3 set swapped).  In read i (0, 1), lane
+          // 16g + 2k + a addresses row 8 (2a + i) + k, groups 8u .. 8u + 7 of
+          // u = g ^ 2a, so lane 16g + 8a + b receives the KM unit of group
+          // 8 (g ^ 2a) + b, octet 2a + i.  Its two units are adjacent in the
+          // KM layout and go back with one 16-byte write once both reads of
+          // the part have landed.  The reads put 32 lanes on 64 distinct
+          // banks (rows 8 apart differ in the half swap, u >> 1 follows a).
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            tb[i] = opaque(msc + 512u * (u32)a + 256u * (u32)i + 32u * (u32)k + 16u * (u32)(((g >> 1) ^ a) ^ i) +
+                           8u * (u32)(g & 1));
+          const int a2 = (lane >> 3) & 1, b = lane & 7;
+          const int pg = 2 * (g ^ (2 * a2)) + (b >> 2) + 8 * (b & 3);
+          tw = opaque(msc + 32u * (u32)pg + 16u * (u32)(a2 ^ (b & 1)));
+        }
+        sel = 0;
+      } else {
+        // MD 16 reads the row's 8 scale bytes of a stage and picks groups gi
+        // and 4 + gi (byte 0x0c of a v_perm selector yields zero); MD 32 reads
+        // the dword of groups 4gi..4gi+3 directly.  Fragment rows are multiples
+        // of 16, so the row swap depends on rr only.
+        const u32 word = G::MD == 32 ? 4u * gi : 0u;
+        const int ssw = (rr >> 3) & 1;
+#pragma unroll
+        for (int g = 0; g < (G::NW == 4 ? 2 : 1); ++g) {
+          bS[0][g] = opaque(lds0 + kScaleBase + (u32)(wm * G::FM * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
+          bS[1][g] =
+              opaque(lds0 + kScaleBase + (u32)(256 + wn * G::FN * G::MD + rr) * kScRowBytes + 16 * (g ^ ssw) + word);
+        }
+        sel = (u32)gi | ((u32)(4 + gi) << 8) | 0x0c0c0000u;
+      }
     } else {
       sel = 0;
     }
@@ -650,6 +769,8 @@ struct Pipe {
   G9_DEV u32 chunk_off(int stage) const {
     if constexpr (I::kPreshuffled)
       return stage < s_end ? (u32)(stage / kScChunk) * cstride : kDeadOff;
+    else if constexpr (I::kKMajor)
+      return stage < s_end ? (u32)stage * 8 * cstride : kDeadOff;
     else
       return stage < s_end ? (u32)stage * 8 : kDeadOff;
   }
@@ -704,12 +825,17 @@ struct Pipe {
       f[F].sp = *(const G9_LDS u32*)(uintptr_t)(base + imm);
   }
 
-  // FP4P: the chunk's scales of every fragment of sub-buffer X from chunk
-  // slot SSLOT (B0 into its registers of chunk parity PAR).
+  // kChunkScales: the chunk's scales of fragment F of sub-buffer X from
+  // chunk slot SSLOT (B0 into its registers of chunk parity PAR).
   template <int X, int SSLOT, int PAR, int F>
-  G9_DEV void read_scales_ps(ScRegs<OP, G>& sr) const {
-    constexpr int imm = SSLOT * kScSlotBytes + (X & 1) * 128 * kScRowBytes + F * G::MD * kScRowBytes;
-    const u32x2 v = *(const G9_LDS u32x2*)(uintptr_t)(bS[X >= 2][0] + imm);
+  G9_DEV void read_chunk_scales(ScRegs<OP, G>& sr) const {
+    u32x2 v;
+    if constexpr (kTrScales<OP, G>) {
+      v = tr_read<SSLOT * kScSlotBytes + (X & 1) * 4096 + (F / 2) * 1024>(bS[X >= 2][F & 1]);
+    } else {
+      constexpr int imm = SSLOT * kScSlotBytes + (X & 1) * 128 * kScRowBytes + F * G::MD * kScRowBytes;
+      v = *(const G9_LDS u32x2*)(uintptr_t)(bS[X >= 2][0] + imm);
+    }
     if constexpr (X == 0)
       sr.a[0][F] = v;
     else if constexpr (X == 1)
@@ -718,6 +844,19 @@ struct Pipe {
       sr.b0[PAR][F] = v;
     else
       sr.b1[F] = v;
+  }
+
+  // kXform: the two transpose reads of part J of this wave's rows in chunk
+  // slot SSLOT, and (a region later, once they have landed) their writes.
+  template <int SSLOT, int J>
+  G9_DEV void xform_read(ScRegs<OP, G>& sr) const {
+    constexpr int imm = SSLOT * kScSlotBytes + J * 1024;
+    sr.t[0] = tr_read<imm>(tb[0]);
+    sr.t[1] = tr_read<imm>(tb[1]);
+  }
+  template <int SSLOT, int J>
+  G9_DEV void xform_write(const ScRegs<OP, G>& sr) const {
+    lds_store16<SSLOT * kScSlotBytes + J * 1024>(tw, sr.t[0], sr.t[1]);
   }
 
   // Whole-set variants for the prologue.  Stage 0 of a K tail: the lanes
@@ -751,7 +890,7 @@ struct Pipe {
     constexpr int NF = X < 2 ? G::FM : G::FN;
     [&]<int... R>(std::integer_sequence<int, R...>) { (read_chunk<X, SLOT, R>(f), ...); }(
         std::make_integer_sequence<int, G::NC * NF>{});
-    if constexpr (I::kScaled && !I::kPreshuffled) {
+    if constexpr (I::kScaled && !kChunkScales<OP, G>) {
       [&]<int... F>(std::integer_sequence<int, F...>) { (read_scales<X, SSLOT, ST, F>(f), ...); }(
           std::make_integer_sequence<int, NF>{});
     }
@@ -801,6 +940,23 @@ G9_DEV void settle_acc(Acc<G>& acc) {
   pin_acc<G>(acc);
 }
 
+// Ends every path out of a stage sequence that issued inline-assembly scale
+// reads (kTrScales): waits for them, then keeps their registers live up to
+// that point, so the compiler neither reuses a register whose LDS read is
+// still in flight (a read whose result a partial body never consumes is dead
+// to it) nor touches one early.  isa_check.py verifies the built code.
+template <Op OP, class G>
+G9_DEV void settle_scales(ScRegs<OP, G>& sr) {
+  if constexpr (kTrScales<OP, G>) {
+    waitcnt<63, 0>();
+    asm volatile("" : "+v"(sr.t[0]), "+v"(sr.t[1]));
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) asm volatile("" : "+v"(sr.a[0][i]), "+v"(sr.a[1][i]));
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) asm volatile("" : "+v"(sr.b1[j]), "+v"(sr.b0[0][j]), "+v"(sr.b0[1][j]));
+  }
+}
+
 // Slot K of the region at body position POS: MFMA number K (step-major: step,
 // A fragment, B fragment), then whatever the slot table puts after it, then a
 // hard scheduling fence (the MFMAs are inline assembly, which the scheduler's
@@ -815,7 +971,7 @@ template <Op OP, class G, int POS, int K>
 G9_DEV void region_mfma(QAcc<G>& acc, const ScRegs<OP, G>& sr, const FragSet<G>& bx, const FragSet<G>& ay) {
   constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j0 = K % G::FN;
   constexpr int j = (i % 2) ? G::FN - 1 - j0 : j0;
-  if constexpr (OpInfo<OP>::kPreshuffled) {
+  if constexpr (kChunkScales<OP, G>) {
     // Region POS % 4 is quadrant (A0,B0), (A0,B1), (A1,B1), (A1,B0); its
     // stage is stage POS / 4 % 4 of chunk POS / 16 of the body.
     constexpr int quad = POS % 4, st = (POS / 4) % kScChunk, cp = (POS / 16) % 2;
@@ -850,12 +1006,12 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
     static_for<S::NR>([&](auto R) {
       if constexpr (S::read_q(decltype(R)::value) == q) P.template read_chunk<RX, RSLOT, decltype(R)::value>(nxt);
     });
-    if constexpr (OpInfo<OP>::kPreshuffled) {
+    if constexpr (kChunkScales<OP, G>) {
       // The chunk's scales of set RX, when RX is read for a chunk's first stage.
       if constexpr (kSt == 0) {
         static_for<NF>([&](auto F) {
           if constexpr (S::scale_q(decltype(F)::value) == q)
-            P.template read_scales_ps<RX, kSSlot, (ks / kScChunk) % 2, decltype(F)::value>(sr);
+            P.template read_chunk_scales<RX, kSSlot, (ks / kScChunk) % 2, decltype(F)::value>(sr);
         });
       }
     } else if constexpr (OpInfo<OP>::kScaled) {
@@ -868,7 +1024,20 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
       if constexpr (S::dma_q(decltype(J)::value) == q) P.template dma_rows<DX, DSLOT, decltype(J)::value>(r, soff, mb);
     });
     if constexpr (part >= 0 && q == S::kScaleDmaQ) P.template dma_chunk<kDSSlot, (part >= 0 ? part : 0)>(soff_sc, ms);
-    if constexpr (OpInfo<OP>::kScaled && !OpInfo<OP>::kPreshuffled && G::MD == 16) {
+    if constexpr (kXform<OP, G>) {
+      // Transpose of the next chunk (slot xs): part j is read at body
+      // position 16h + R(j), R = 5, 8, 10, 12 -- at least 7 regions after its
+      // DMA (16h - 2 + 2j), which the region-start vmcnt wait has completed
+      // -- and written one region later, in the same stage, so a partial
+      // body never stops between the two.  The last writes land before the
+      // barrier of position 16h + 14, whose region first reads the chunk.
+      constexpr int p16 = POS % 16, xs = (POS / 16 + 1) % 2;
+      constexpr int rj = p16 == 5 ? 0 : p16 == 8 ? 1 : p16 == 10 ? 2 : p16 == 12 ? 3 : -1;
+      constexpr int wj = p16 == 6 ? 0 : p16 == 9 ? 1 : p16 == 11 ? 2 : p16 == 13 ? 3 : -1;
+      if constexpr (rj >= 0 && q == S::kXformQ) P.template xform_read<xs, (rj >= 0 ? rj : 0)>(sr);
+      if constexpr (wj >= 0 && q == S::kXformQ) P.template xform_write<xs, (wj >= 0 ? wj : 0)>(sr);
+    }
+    if constexpr (OpInfo<OP>::kScaled && !kChunkScales<OP, G> && G::MD == 16) {
       static_for<NF>([&](auto F) {
         constexpr int f = decltype(F)::value;
         if constexpr (S::perm_q(f) == q) {
@@ -952,7 +1121,7 @@ G9_DEV void region_pp(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<
                       const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using Sh = Shape<OP, G>;
-  static_assert(!OpInfo<OP>::kPreshuffled, "preshuffled scales run 4-wave");
+  static_assert(!kChunkScales<OP, G>, "chunk-wide scale reads run 4-wave");
   constexpr int ks = POS / 4 + (POS % 4 >= 2 ? 1 : 0);
   constexpr int kSSlot = (ks / kScChunk) % 2, kSt = ks % kScChunk;
   constexpr int part = Sh::sc_part(POS);
@@ -1053,20 +1222,30 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   // then (once every wave has) refill A0 slot 0 with stage s0+2.  Ping-pong:
   // B1(s0) as well, which the first memory cluster reads.
   constexpr int kFirst = (kPingPong<G> ? 5 : 6) * Sh::D + (kScaled ? 1 : 0);
+  ScRegs<OP, G> sr;
   waitcnt<kFirst, 0>();
+  if constexpr (kXform<OP, G>) {
+    // This wave's parts of chunk 0 have landed: transpose them before any
+    // wave reads the chunk (the barrier below), all reads first (one LDS
+    // round trip for the chunk, in registers the loop has not claimed yet).
+    ScRegs<OP, G> xs[G::kScParts];
+    static_for<G::kScParts>([&](auto J) { P.template xform_read<0, decltype(J)::value>(xs[J]); });
+    waitcnt<63, 0>();
+    static_for<G::kScParts>([&](auto J) { P.template xform_write<0, decltype(J)::value>(xs[J]); });
+    waitcnt<63, 0>();
+  }
   barrier();
   FragSet<G> at, ab, x, y;
-  ScRegs<OP, G> sr;
   P.template load<0, 0, 0, 0>(at);
   P.template load<2, 0, 0, 0>(x);
-  if constexpr (OpInfo<OP>::kPreshuffled) {
+  if constexpr (kChunkScales<OP, G>) {
     // Chunk 0's scales of A0 and B0 (read by body positions -2 and -1 in the
     // steady state); B1's and A1's follow in the first two regions.
-    static_for<G::FM>([&](auto F) { P.template read_scales_ps<0, 0, 0, decltype(F)::value>(sr); });
-    static_for<G::FN>([&](auto F) { P.template read_scales_ps<2, 0, 0, decltype(F)::value>(sr); });
+    static_for<G::FM>([&](auto F) { P.template read_chunk_scales<0, 0, 0, decltype(F)::value>(sr); });
+    static_for<G::FN>([&](auto F) { P.template read_chunk_scales<2, 0, 0, decltype(F)::value>(sr); });
   }
   waitcnt<kFirst, 0>();
-  if constexpr (kScaled && !OpInfo<OP>::kPreshuffled && G::MD == 16) {
+  if constexpr (kScaled && !kChunkScales<OP, G> && G::MD == 16) {
     P.template gather_scales<0>(at);
     P.template gather_scales<2>(x);
   }
@@ -1084,9 +1263,11 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
   int s = s0;
   for (; s + Sh::kBody <= s1; s += Sh::kBody)
     static_for<Sh::kBody>([&](auto K) { stage<OP, G, decltype(K)::value>(P, s, acc, sr, at, ab, x, y); });
+  settle_scales<OP, G>(sr);
   settle_acc<G>(acc);
   if (s < s1) {
     tail<OP, G, 0>(P, s, s1 - s, acc, sr, at, ab, x, y);
+    settle_scales<OP, G>(sr);
     settle_acc<G>(acc);
   }
   if constexpr (kPingPong<G>) {
@@ -1286,7 +1467,6 @@ G9_DEV void gemm_moe(const GemmParams& p) {
 // range from the last tile backwards, so the prefix it owes a successor is
 // produced first and the suffix it inherits is consumed last.
 // ---------------------------------------------------------------------------
-constexpr u32 kSpinLimit = 1u << 26;
 
 // Index (in f32x4) of a wave's fragment in a tile's partial: the accumulator
 // register layout, so each wave access is a contiguous KiB.
@@ -1303,8 +1483,12 @@ G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
   while (__builtin_amdgcn_readfirstlane(
              __hip_atomic_load(p.flags + tile, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != want) {
     __builtin_amdgcn_s_sleep(2);
-    if (++spins > kSpinLimit) {
+    if (++spins > p.spin_limit) {
       __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The host flag of g9_workspace_watch (a device-writable host int, or
+      // null), so the caller sees the failure without synchronising.
+      int* host = *reinterpret_cast<int* const*>(reinterpret_cast<const char*>(p.err) + 8);
+      if (host) __hip_atomic_store(host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       break;
     }
   }

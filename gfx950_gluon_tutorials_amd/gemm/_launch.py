@@ -110,11 +110,26 @@ class _Workspaces:
     A workspace is only ever used by launches on its own stream, which the
     stream orders, so launches on different streams never share partials or
     flags.  Each workspace is allocated while its stream is current, so the
-    caching allocator ties the memory to that stream as well."""
+    caching allocator ties the memory to that stream as well.
+
+    Each workspace has a pinned host int registered with g9_workspace_watch:
+    a launch whose flag wait times out sets it, and the next stream-K launch
+    on that stream (or ``poll``) raises, with no synchronisation."""
 
     def __init__(self):
         self._lock = threading.Lock()
         self._ws: dict[tuple[int, int], torch.Tensor] = {}
+        self._flag: dict[tuple[int, int], torch.Tensor] = {}
+
+    def _init(self, ws: torch.Tensor, key, stream: int) -> None:
+        lib = _lib.load()
+        _lib.check(lib.g9_workspace_init(ws.data_ptr(), ws.numel(), stream), "workspace init")
+        flag = self._flag.get(key)
+        if flag is None:
+            flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+            self._flag[key] = flag
+        flag.zero_()
+        _lib.check(lib.g9_workspace_watch(ws.data_ptr(), ws.numel(), flag.data_ptr(), stream), "workspace watch")
 
     def get(self, dev: torch.device, nbytes: int, stream: int) -> tuple[int, int]:
         if nbytes == 0:
@@ -124,9 +139,24 @@ class _Workspaces:
             ws = self._ws.get(key)
             if ws is None or ws.numel() < nbytes:
                 ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-                _lib.check(_lib.load().g9_workspace_init(ws.data_ptr(), ws.numel(), stream), "workspace init")
+                self._init(ws, key, stream)
                 self._ws[key] = ws
         return ws.data_ptr(), ws.numel()
+
+    def poll(self, dev: torch.device, stream: int | None = None) -> None:
+        """Raises RuntimeError if a stream-K launch on `stream` has timed out
+        in a flag wait since the last check (without synchronising: launches
+        still running are seen by a later poll), after clearing the
+        workspace so later launches start clean."""
+        s = _stream(dev) if stream is None else int(stream)
+        key = (_dev_index(dev), s)
+        flag = self._flag.get(key)
+        if flag is None or int(flag[0]) == 0:
+            return
+        with self._lock:
+            self._init(self._ws[key], key, s)
+        raise RuntimeError(f"a stream-K flag wait timed out on {dev} (stream {s:#x}) since the last check; "
+                           "that launch's output is wrong")
 
     def error(self, dev: torch.device, stream: int | None = None) -> int:
         """Synchronises `stream` (default: the device's current stream) and
@@ -148,8 +178,9 @@ class _Workspaces:
         err = self.error(dev, stream)
         if err:
             s = _stream(dev) if stream is None else int(stream)
-            ws = self._ws[(_dev_index(dev), s)]
-            _lib.check(_lib.load().g9_workspace_init(ws.data_ptr(), ws.numel(), s), "workspace init")
+            key = (_dev_index(dev), s)
+            with self._lock:
+                self._init(self._ws[key], key, s)
             raise RuntimeError(f"stream-K flag wait timed out on {dev} (error word {err}); that output is wrong")
 
     def release(self) -> None:
@@ -157,16 +188,21 @@ class _Workspaces:
         caching allocator once the streams that used it are done)."""
         with self._lock:
             self._ws.clear()
+            self._flag.clear()
 
 
 WORKSPACES = _Workspaces()
 
-# G9_CHECK=1: after every stream-K launch, synchronise its stream and raise if
-# a flag wait timed out (a debugging aid: it serialises the host with the GPU).
+# Every stream-K launch first polls its workspace's host flag, so a timed-out
+# flag wait of an earlier launch on the stream raises at the next one.
+# G9_CHECK=1 also synchronises after every stream-K launch and raises for that
+# launch itself (a debugging aid: it serialises the host with the GPU).
 CHECK_STREAMK = os.environ.get("G9_CHECK", "0") not in ("", "0")
 
 
 def _workspace(lib, dt: int, M: int, N: int, K: int, sched: int, waves: int, dev, stream) -> tuple[int, int]:
+    if sched == _lib.G9_SCHED_SK:
+        WORKSPACES.poll(dev, stream)
     need = lib.g9_workspace_size(dt, M, N, K, sched, waves)
     return WORKSPACES.get(dev, need, stream)
 
@@ -247,6 +283,13 @@ def _scales_ok(s: torch.Tensor) -> bool:
     return s.stride(1) == 1 and s.stride(0) % 4 == 0 and s.stride(0) >= s.shape[1] and s.data_ptr() % 4 == 0
 
 
+def _kmajor_scales_ok(s: torch.Tensor) -> bool:
+    """A K-major (rows contiguous, one group after another) scale view, as the
+    reference bench's ``randint((K // 32, M)).T`` produces."""
+    return (s.shape[1] > 1 and s.stride(0) == 1 and s.stride(1) % 4 == 0 and s.stride(1) >= s.shape[0]
+            and s.data_ptr() % 4 == 0)
+
+
 def _ps_scales_ok(s: torch.Tensor) -> bool:
     return s.stride(2) == 1 and s.stride(1) == 32 and s.stride(0) % 16 == 0 and s.data_ptr() % 16 == 0
 
@@ -303,13 +346,18 @@ def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales
     if a_scales.shape != (M, K // 32) or b_scales.shape != (N, K // 32):
         raise ValueError(f"scales must be ({M}, {K // 32}) and ({N}, {K // 32}); got "
                          f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
-    if not _scales_ok(a_scales):
-        a_scales = a_scales.contiguous()
-    if not _scales_ok(b_scales):
-        b_scales = b_scales.contiguous()
+    # K-major scale views (both operands) go to the 4-wave kernels as they
+    # are; anything else is read row-major, repacked if need be.
+    kmajor = waves == 4 and _kmajor_scales_ok(a_scales) and _kmajor_scales_ok(b_scales)
+    if not kmajor:
+        if not _scales_ok(a_scales):
+            a_scales = a_scales.contiguous()
+        if not _scales_ok(b_scales):
+            b_scales = b_scales.contiguous()
+    dt = _lib.G9_FP4K if kmajor else _lib.G9_FP4
     sched = _schedule_code(schedule, M, N, _lib.G9_FP4)
     stream = _stream(dev)
-    ws, ws_bytes = _workspace(lib, _lib.G9_FP4, M, N, K, sched, waves, dev, stream)
+    ws, ws_bytes = _workspace(lib, dt, M, N, K, sched, waves, dev, stream)
     rc = lib.g9_gemm_a4w4(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(),
                           M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
                           c.stride(0), c.stride(1), a_scales.stride(0), a_scales.stride(1),

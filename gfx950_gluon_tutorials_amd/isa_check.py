@@ -20,6 +20,14 @@ Each instruction counts one wait state, ``s_nop N`` counts N + 1.  The scan is
 a fixed-point over the basic blocks (labels and branches), so hazards that
 cross a branch or a loop back edge are seen.
 
+A second scan covers LDS reads the compiler does not track (the transpose
+reads of the MXFP4 scale chunks are inline assembly): a VGPR written by a
+``ds_*`` read is pending until an ``s_waitcnt lgkmcnt(k)`` with at least k DS
+instructions issued after that read (DS operations complete in order), and
+no instruction may read or write it while it is pending.  Compiler-generated
+LDS reads satisfy this by construction; the scan proves it for the inline
+ones.
+
 Usage: ``python -m gfx950_gluon_tutorials_amd.isa_check file.s`` (exit status 1
 on violations), or ``check_text(asm) -> list of violations``.
 """
@@ -190,6 +198,57 @@ def _step(state: dict, ins: Instr, violations: list, func: str):
             state[r] = (MFMA_AFTER_VALU, ins.line, False)
 
 
+_LGKM = re.compile(r"lgkmcnt\((\d+)\)")
+
+
+def _lgkm_wait(ins: Instr) -> int | None:
+    """The lgkmcnt limit of an s_waitcnt (None if it does not constrain it)."""
+    if ins.mnemonic != "s_waitcnt":
+        return None
+    ops = ins.text.split(None, 1)[1] if " " in ins.text else ""
+    m = _LGKM.search(ops)
+    if m:
+        return int(m.group(1))
+    try:
+        v = int(ops.strip(), 0)  # raw gfx9 encoding: lgkmcnt in bits 11:8
+    except ValueError:
+        return None
+    k = (v >> 8) & 15
+    return None if k == 15 else k
+
+
+def _lds_step(state: dict, ins: Instr, violations: list, func: str):
+    """Advances the pending-LDS-result state over one instruction.
+
+    state maps a VGPR to (DS instructions issued since the read, read line)."""
+    for r in sorted(ins.dst | ins.src):
+        ent = state.get(r)
+        if ent:
+            violations.append(
+                f"{func}: line {ins.line + 1}: '{ins.text}' touches {r[0]}{r[1]} before the LDS read at line "
+                f"{ent[1] + 1} is waited for"
+            )
+            break
+    k = _lgkm_wait(ins)
+    if k is not None:
+        for r in [r for r, ent in state.items() if ent[0] >= k]:
+            del state[r]
+    if ins.mnemonic.startswith("ds_"):
+        for r in list(state):
+            state[r] = (state[r][0] + 1, state[r][1])
+        if not ins.mnemonic.startswith("ds_write"):
+            for r in ins.dst:
+                state[r] = (0, ins.line)
+
+
+def _merge_lds(a: dict, b: dict) -> dict:
+    out = dict(a)
+    for r, ent in b.items():
+        if r not in out or out[r][0] > ent[0]:
+            out[r] = ent
+    return out
+
+
 def _merge(a: dict, b: dict) -> dict:
     out = dict(a)
     for r, ent in b.items():
@@ -198,8 +257,7 @@ def _merge(a: dict, b: dict) -> dict:
     return out
 
 
-def check_function(name: str, lines: list[str]) -> list[str]:
-    blocks = _blocks(lines)
+def _fixpoint(name: str, blocks, step, merge) -> list[str]:
     entry_state = [None] * len(blocks)
     entry_state[0] = {}
     work = [0]
@@ -211,15 +269,20 @@ def check_function(name: str, lines: list[str]) -> list[str]:
         state = dict(entry_state[k])
         v: list[str] = []
         for ins in blocks[k][1]:
-            _step(state, ins, v, name)
+            step(state, ins, v, name)
         for msg in v:
             seen_violations.setdefault(msg, None)
         for s in blocks[k][2]:
-            new = state if entry_state[s] is None else _merge(entry_state[s], state)
+            new = state if entry_state[s] is None else merge(entry_state[s], state)
             if new != entry_state[s]:
                 entry_state[s] = new
                 work.append(s)
     return list(seen_violations)
+
+
+def check_function(name: str, lines: list[str]) -> list[str]:
+    blocks = _blocks(lines)
+    return _fixpoint(name, blocks, _step, _merge) + _fixpoint(name, blocks, _lds_step, _merge_lds)
 
 
 def check_text(asm: str) -> list[str]:

@@ -45,7 +45,7 @@ import sys
 import numpy as np
 
 CYCLES_PER_STAGE = 2048
-STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256, "mxfp4ps": 256}
+STAGE_K = {"fp16": 64, "bf16": 64, "bf8": 128, "mxfp4": 256, "mxfp4ps": 256, "mxfp4km": 256}
 REALTIME_HZ = 100e6
 NUM_XCDS = 8
 
@@ -112,6 +112,8 @@ def _inputs(dtype: str, M: int, N: int, K: int, dev, seed: int = 0):
     pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=g).to(dev))
     if dtype == "mxfp4ps":  # preshuffled scales (g9_gemm_a4w4_preshuffled)
         sa, sb = quant.preshuffle_e8m0(sa), quant.preshuffle_e8m0(sb)
+    if dtype == "mxfp4km":  # K-major scale views, as the reference bench passes them
+        sa, sb = sa.t().contiguous().t(), sb.t().contiguous().t()
     return pa, pb, sa, sb, torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
 

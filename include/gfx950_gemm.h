@@ -47,8 +47,10 @@ enum {
 };
 
 /* Element / output types.  G9_FP4P is MXFP4 with preshuffled scales (the
- * operand type of g9_gemm_a4w4_preshuffled, for g9_kernel_name). */
-enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3, G9_FP4P = 4 };
+ * operand type of g9_gemm_a4w4_preshuffled) and G9_FP4K MXFP4 with K-major
+ * scales (g9_gemm_a4w4 given K-major scale views), both for g9_kernel_name
+ * and g9_workspace_size. */
+enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3, G9_FP4P = 4, G9_FP4K = 5 };
 
 /* Tile schedules.  G9_SCHED_SPLITK has no counterpart in the reference: it is
  * for callers whose grids leave most CUs idle (few-row GEMMs, one GPU's
@@ -84,14 +86,24 @@ int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, 
  * and error words with a fill kernel on `stream` (no memset), split-K writes
  * every partial it reads.  Calls share their GPU's array, so calls that may
  * overlap on one GPU (other streams, other host threads) race and must be
- * ordered by the caller.  A stream-K flag wait that times out (only possible
- * when calls overlap) leaves a wrong output and is not reported.
+ * ordered by the caller.  A stream-K flag wait that times out leaves a wrong
+ * output; g9_noalloc_error reports it.
  */
 #define G9_NOALLOC_MAX_TILES 256
 int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
                            int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
                            int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
                            void* stream);
+
+/*
+ * Error word of the static array of g9_gemm_a16w16_noalloc on the device of
+ * `stream`, copied to *error after synchronising `stream`: 1 when a flag wait
+ * of the last stream-K call there timed out (that call's output is wrong),
+ * else 0.  Each stream-K call clears it first, so read it before the next
+ * one.  For the same callers as g9_gemm_a16w16_noalloc; allocates nothing.
+ * No counterpart in the reference.
+ */
+int g9_noalloc_error(void* stream, int* error);
 
 /*
  * a8w8: BF8 (fp8 e5m2) in, fp32 accumulate, C = (A.B) * a_scale[0] * b_scale[0]
@@ -113,7 +125,11 @@ int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, in
  * byte, low nibble = even k); a_scales is M x K/32 and b_scales N x K/32 E8M0
  * bytes (2^(x-127)).  K is the logical (unpacked) depth, a multiple of 256.
  * Strides are in bytes.  Output `out_dtype` (G9_BF16, the reference default,
- * or G9_F16).
+ * or G9_F16).  The scales are row-major (stride_ask = stride_bsk = 1, row
+ * strides multiples of 4), or both K-major (stride_asm = stride_bsn = 1,
+ * group strides multiples of 4 of at least M and N bytes: the transposed
+ * (K/32, M) storage the reference bench passes as its scale views), which the
+ * 4-wave kernels read as they are (G9_ERR_SCHEDULE with `waves` = 8).
  * Replaces kernels/gemm/intra_wave/a4w4/v1_sliceMN/matmul_kernel.py:696-742 (4-wave)
  * and kernels/gemm/inter_wave/a4w4/v2_mfma32x32x64/matmul_kernel.py:614-668 (8-wave).
  */
@@ -209,6 +225,25 @@ int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
  * the reference.
  */
 int g9_workspace_error(const void* workspace, size_t workspace_bytes, void* stream, int* error);
+
+/*
+ * Registers `host_flag`, an int in host memory the device can write (pinned:
+ * hipHostMalloc), with a stream-K workspace: a launch whose flag wait times
+ * out then also stores 1 there, so the caller learns of it without
+ * synchronising (for instance by reading it before each launch).  Enqueued on
+ * `stream` after g9_workspace_init, which clears the registration; NULL
+ * removes it.  No counterpart in the reference.
+ */
+int g9_workspace_watch(void* workspace, size_t workspace_bytes, int* host_flag, void* stream);
+
+/*
+ * Polls a stream-K flag wait makes before it gives up, sets the error word
+ * and carries on with whatever partial the workspace holds (0 restores the
+ * default, 2^26, seconds of waiting).  Returns the previous value.  For tests
+ * of the timeout path: a tiny limit makes waits time out while every
+ * workgroup still exits normally.  Applies to launches made after the call.
+ */
+uint32_t g9_set_streamk_spin_limit(uint32_t polls);
 
 /*
  * Name of the kernel a call with this (dtype, out_dtype, schedule, waves)

@@ -375,3 +375,78 @@ def simulate_streamk(tiles: int, stages: int, ctas: int):
     if not all(all(r) for r in done):
         raise AssertionError("some (tile, stage) never computed")
     return step, flag
+
+
+def streamk_cta_of_block(block: int, ctas: int, num_xcds: int = 8) -> int:
+    """The stream-K range a workgroup takes: gemm_sk renumbers blockIdx with
+    the XCD remap of get_pids (one contiguous run of ranges per XCD, group size
+    1), so block b, dispatched to XCD b % num_xcds, owns range new_id[b]."""
+    if num_xcds == 1:
+        return block
+    pid_m, _ = get_pids(block, ctas, 1, 1, 1, ctas, num_xcds, 1)
+    return pid_m
+
+
+def simulate_streamk_dispatch(tiles: int, stages: int, ctas: int, resident, num_xcds: int = 8,
+                              cta_of_block=None):
+    """The stream-K chain protocol under partial residency (other kernels
+    holding CUs): workgroup b goes to XCD b % num_xcds, each XCD starts its
+    workgroups in increasing b as slots free up, at most resident[x] of them
+    at once (resident[x] >= 1), and a workgroup holds its slot while it waits
+    for a predecessor's flag.  Each step, every resident workgroup whose
+    current segment may run advances one stage; a finished workgroup frees its
+    slot.  Returns the makespan in stage-steps; raises AssertionError if the
+    workgroups deadlock or a stage is covered twice or never.
+
+    cta_of_block maps a workgroup to its range (default: gemm_sk's XCD remap)."""
+    if cta_of_block is None:
+        cta_of_block = lambda b: streamk_cta_of_block(b, ctas, num_xcds)  # noqa: E731
+    segs = streamk_segments(tiles, stages, ctas)
+    queues = [[b for b in range(x, ctas, num_xcds)] for x in range(num_xcds)]
+    running: list[list[int]] = [[] for _ in range(num_xcds)]
+    flag = [0] * tiles
+    done = [[False] * stages for _ in range(tiles)]
+    pos = {}
+    prog = {}
+    step = 0
+    finished = 0
+    while finished < ctas:
+        for x in range(num_xcds):  # dispatch in block order into free slots
+            while queues[x] and len(running[x]) < resident[x]:
+                b = queues[x].pop(0)
+                c = cta_of_block(b)
+                running[x].append(c)
+                pos[c], prog[c] = 0, 0
+        moved = False
+        advance = []
+        for x in range(num_xcds):
+            for c in running[x]:
+                if pos[c] >= len(segs[c]):
+                    continue
+                t, sb, se = segs[c][pos[c]]
+                if prog[c] == 0 and sb > 0 and flag[t] != sb:
+                    continue
+                advance.append(c)
+        for c in advance:
+            t, sb, se = segs[c][pos[c]]
+            s = sb + prog[c]
+            if done[t][s]:
+                raise AssertionError(f"stage {s} of tile {t} covered twice")
+            done[t][s] = True
+            prog[c] += 1
+            moved = True
+            if sb + prog[c] == se:
+                flag[t] = se
+                pos[c] += 1
+                prog[c] = 0
+        for x in range(num_xcds):
+            left = [c for c in running[x] if pos[c] < len(segs[c])]
+            finished += len(running[x]) - len(left)
+            moved = moved or len(left) != len(running[x])
+            running[x] = left
+        step += 1
+        if not moved:
+            raise AssertionError("stream-K workgroups deadlocked")
+    if not all(all(r) for r in done):
+        raise AssertionError("some (tile, stage) never computed")
+    return step

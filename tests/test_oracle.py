@@ -281,3 +281,40 @@ def test_torch_matmul_f32_against_brute_force():
     y = rng.standard_normal((3, 40)).astype(np.float32)
     ref = np.array([[sum(float(x[i, k]) * float(y[j, k]) for k in range(40)) for j in range(3)] for i in range(6)])
     np.testing.assert_allclose(R.torch_matmul_f32(x, y).numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+# --- stream-K progress when not every workgroup is resident ------------------
+#
+# gemm_sk assumes no co-residency.  Workgroup b is dispatched to XCD b % 8
+# and each XCD starts its workgroups in increasing b; the XCD remap gives XCD x
+# the contiguous ranges 32x .. 32x + 31 in that order.  A range waits only on
+# its predecessor, which is either earlier on the same XCD (started before it,
+# so resident or finished) or, for XCD x's first range, the last range of XCD
+# x - 1.  By induction over the XCDs every range finishes as long as each XCD
+# eventually has one free CU; the simulation checks it for the BASELINE
+# stream-K shapes and others under many residency limits.
+
+@pytest.mark.parametrize("tiles,stages", [(225, 256), (160, 128), (16, 256), (32, 128), (272, 128), (400, 128)])
+def test_streamk_progress_under_partial_residency(tiles, stages):
+    rng = np.random.default_rng(tiles * 1000 + stages)
+    limits = [[1] * 8, [2] * 8, [32] * 8, [1, 32] * 4, [32, 1] * 4] + [list(rng.integers(1, 33, 8)) for _ in range(4)]
+    for res in limits:
+        steps = R.simulate_streamk_dispatch(tiles, stages, 256, res)
+        assert steps >= max(stages, -(-tiles * stages // 256))
+
+
+def test_streamk_cta_of_block_is_the_device_remap():
+    # XCD x's blocks (x, x + 8, ...) own the contiguous ranges 32x .. 32x + 31,
+    # in dispatch order; uneven grids give the first XCDs one more.
+    assert [R.streamk_cta_of_block(b, 256) for b in range(0, 256, 8)] == list(range(32))
+    assert [R.streamk_cta_of_block(b, 256) for b in range(3, 256, 8)] == list(range(96, 128))
+    got = sorted(R.streamk_cta_of_block(b, 250) for b in range(250))
+    assert got == list(range(250))
+    assert [R.streamk_cta_of_block(b, 250) for b in range(1, 250, 8)] == list(range(32, 64))
+
+
+def test_streamk_dispatch_simulation_detects_a_deadlock():
+    # Planted mistake: ranges handed out in reverse dispatch order, so a
+    # resident workgroup waits on a predecessor queued behind it on its XCD.
+    with pytest.raises(AssertionError, match="deadlocked"):
+        R.simulate_streamk_dispatch(16, 256, 256, [1] * 8, cta_of_block=lambda b: 255 - b)

@@ -102,3 +102,33 @@ def test_misaligned_b_view_is_repacked(gpu):
     want = _launch.gemm_a16w16(a, b_nk.contiguous().T, torch.empty(M, N, dtype=torch.float16, device=gpu))
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_timed_out_flag_wait_raises_at_the_next_launch(gpu):
+    """A stream-K flag wait that gives up (forced from the host with a spin
+    limit of one poll; every workgroup still exits) sets the workspace's
+    pinned host flag, and the next stream-K launch on that stream raises
+    without any synchronisation of its own.  The workspace is cleared, so the
+    launch after that is bit-identical to data-parallel again."""
+    from gfx950_gluon_tutorials_amd import _lib
+
+    g = torch.Generator().manual_seed(67)
+    M, N, K = 2048, 2048, 8192  # 64 tiles x 128 stages over 256 workgroups: chained waits
+    a, b = _operands(g, M, N, K, gpu)
+    dp = _launch.gemm_a16w16(a, b.T, torch.empty(M, N, dtype=torch.float16, device=gpu))
+    lib = _lib.load()
+    _say("stream-K with a spin limit of one poll")
+    prev = lib.g9_set_streamk_spin_limit(1)
+    try:
+        _launch.gemm_a16w16(a, b.T, torch.empty(M, N, dtype=torch.float16, device=gpu), schedule="streamk")
+        torch.cuda.synchronize()
+    finally:
+        lib.g9_set_streamk_spin_limit(prev)
+    _say("next stream-K launch raises")
+    with pytest.raises(RuntimeError, match="timed out"):
+        _launch.gemm_a16w16(a, b.T, torch.empty(M, N, dtype=torch.float16, device=gpu), schedule="streamk")
+    _say("and the one after is right")
+    c = _launch.gemm_a16w16(a, b.T, torch.empty(M, N, dtype=torch.float16, device=gpu), schedule="streamk")
+    torch.cuda.synchronize()
+    assert torch.equal(c, dp)
+    _launch.WORKSPACES.poll(gpu)  # nothing pending

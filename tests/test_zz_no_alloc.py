@@ -111,3 +111,66 @@ def test_noalloc_rejects_more_than_the_scratch_holds(gpu):
     assert _call("noalloc", a, b, c, _lib.G9_F16, _lib.G9_SCHED_DP, 4) == 0
     torch.cuda.synchronize()
     assert torch.equal(c, _with_workspace(a, b, _lib.G9_F16, _lib.G9_SCHED_DP, 4))
+
+
+def _noalloc_error(dev):
+    out = _lib.ctypes.c_int(-1)
+    assert _lib.load().g9_noalloc_error(torch.cuda.current_stream(dev).cuda_stream, _lib.ctypes.byref(out)) == 0
+    return out.value
+
+
+def test_noalloc_reports_a_timed_out_flag_wait(gpu):
+    """g9_noalloc_error reads the static array's error word.  A spin limit of
+    one poll (set from the host) makes the chained waits of a stream-K call
+    time out while every workgroup still exits; the call's output is then
+    wrong and the word reads 1.  With the default limit the next call clears
+    it, reads 0 and matches the workspace entry point again."""
+    g = torch.Generator().manual_seed(83)
+    M, N, K = 2048, 2048, 8192  # 64 tiles x 128 stages over 256 workgroups: 4 per tile, chained
+    a, b = _operands(g, M, N, K, torch.float16, gpu)
+    want = _with_workspace(a, b, _lib.G9_F16, _lib.G9_SCHED_SK, 4)
+    c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    lib = _lib.load()
+    _say("noalloc stream-K, default spin limit: error word 0")
+    assert _call("noalloc", a, b, c, _lib.G9_F16, _lib.G9_SCHED_SK, 4) == 0
+    assert _noalloc_error(gpu) == 0
+    assert torch.equal(c, want)
+    _say("noalloc stream-K, spin limit 1: error word 1")
+    prev = lib.g9_set_streamk_spin_limit(1)
+    try:
+        assert _call("noalloc", a, b, c, _lib.G9_F16, _lib.G9_SCHED_SK, 4) == 0
+        assert _noalloc_error(gpu) == 1
+    finally:
+        lib.g9_set_streamk_spin_limit(prev)
+    _say("noalloc stream-K, default spin limit again: error word 0, output right")
+    assert _call("noalloc", a, b, c, _lib.G9_F16, _lib.G9_SCHED_SK, 4) == 0
+    assert _noalloc_error(gpu) == 0
+    assert torch.equal(c, want)
+
+
+@pytest.mark.parametrize("sched,shape", [(_lib.G9_SCHED_SK, (3840, 3840, 2048)),
+                                         (_lib.G9_SCHED_SPLITK, (512, 4096, 8192))])
+def test_noalloc_under_graph_capture(gpu, sched, shape):
+    """One call captured in a HIP graph (its stream-K flag clearing is a fill
+    kernel, not a memset) and replayed three times with eager work and
+    synchronisations in between: every replay is bit-equal to the workspace
+    entry point."""
+    g = torch.Generator().manual_seed(90 + sched)
+    M, N, K = shape
+    a, b = _operands(g, M, N, K, torch.float16, gpu)
+    want = _with_workspace(a, b, _lib.G9_F16, sched, 4)
+    c = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    _say(f"noalloc schedule={sched} {M}x{N}x{K}: eager call, then capture")
+    assert _call("noalloc", a, b, c, _lib.G9_F16, sched, 4) == 0  # looks up the array outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _call("noalloc", a, b, c, _lib.G9_F16, sched, 4)
+    assert rc == 0
+    for r in range(3):
+        _say(f"noalloc schedule={sched}: replay {r}")
+        c.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, want), r
