@@ -35,18 +35,24 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 # Published dense MFMA peaks of one MI355X, TFLOP/s.
-PEAK = {"fp16": 2500.0, "bf16": 2500.0, "bf8": 5000.0, "mxfp4": 10100.0, "mxfp4ps": 10100.0}
+PEAK = {"fp16": 2500.0, "bf16": 2500.0, "bf8": 5000.0, "mxfp4": 10100.0, "mxfp4ps": 10100.0, "mxfp4km": 10100.0}
 # The reference's published MI355X numbers for the same shapes (4-wave,
 # kernels/gemm/intra_wave/a16w16/v9_beyond_hotloop/README.md:180,
 # kernels/gemm/inter_wave/a8w8/README.md:61, kernels/gemm/inter_wave/a4w4/v0_sliceMN/README.md:60).
-REFERENCE_TFLOPS = {"fp16": 1608.0, "bf8": 3215.0, "mxfp4": 4986.0, "mxfp4ps": 4986.0}
+REFERENCE_TFLOPS = {"fp16": 1608.0, "bf8": 3215.0, "mxfp4": 4986.0, "mxfp4ps": 4986.0, "mxfp4km": 4986.0}
 # 8-wave: kernels/gemm/inter_wave/a16w16/README.md:120, kernels/gemm/inter_wave/a8w8/README.md:61,
 # kernels/gemm/inter_wave/a4w4/README.md:17.
 REFERENCE_TFLOPS_8W = {"fp16": 1478.0, "bf8": 2949.0, "mxfp4": 4479.0}
 # BF16 and the headline-K shapes (4-wave, 8-wave): scripts/plot_perf_summary.py:53-58.
 REFERENCE_TFLOPS["bf16"] = 1696.0
 REFERENCE_TFLOPS_8W["bf16"] = 1573.6
-HEADLINE_K = {"bf8": (16384, 3476.0, 3131.1), "mxfp4": (32768, 5804.0, 5195.9), "mxfp4ps": (32768, 5804.0, None)}
+HEADLINE_K = {"bf8": (16384, 3476.0, 3131.1), "mxfp4": (32768, 5804.0, 5195.9), "mxfp4ps": (32768, 5804.0, None),
+              "mxfp4km": (32768, 5804.0, None)}
+# MXFP4 scale layouts: mxfp4 row-major (M x K/32 bytes, BASELINE's configuration),
+# mxfp4km K-major views of (K/32, M) storage (what the reference bench passes,
+# kernels/gemm/intra_wave/a4w4/bench.py:137-146), mxfp4ps preshuffled.  Only
+# the 4-wave kernels read the last two as they are.
+FOUR_WAVE_ONLY = ("mxfp4ps", "mxfp4km")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 # Flash-attention forward: the reference's tuned shape and its published
 # numbers (bf16, kernels/attention/README.md:619-632; no fp16 figure).
@@ -66,8 +72,9 @@ def parse_args():
     p.add_argument("--settle-ms", type=float, default=600.0,
                    help="keep warming up until this much time has passed (the MI355X's clocks take a few "
                         "hundred ms of load to settle; timed launches before that run up to 15%% slower)")
-    p.add_argument("--dtypes", default="fp16,bf16,bf8,mxfp4,mxfp4ps",
-                   help="comma list of fp16,bf16,bf8,mxfp4,mxfp4ps (mxfp4 with preshuffled scales, 4-wave)")
+    p.add_argument("--dtypes", default="fp16,bf16,bf8,mxfp4,mxfp4km,mxfp4ps",
+                   help="comma list of fp16,bf16,bf8,mxfp4,mxfp4km,mxfp4ps (mxfp4 with K-major scale views as the "
+                        "reference bench passes them / with preshuffled scales, 4-wave)")
     p.add_argument("--headline-k", type=int, default=1,
                    help="also time bf8 at K=16384 and mxfp4 at K=32768, the reference's headline shapes")
     p.add_argument("--streamk", type=int, default=1, help="also time the stream-K shapes (0/1)")
@@ -152,11 +159,13 @@ def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int, wa
             qa, sa = quant.quantize_e5m2(torch.randn(M, K, generator=gen).to(dev))
             qb, sb = quant.quantize_e5m2(torch.randn(N, K, generator=gen).to(dev))
             sets.append((qa, qb.T, sa, sb))
-        elif dtype in ("mxfp4", "mxfp4ps"):
+        elif dtype in ("mxfp4", "mxfp4ps", "mxfp4km"):
             pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=gen).to(dev))
             pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=gen).to(dev))
             if dtype == "mxfp4ps":  # the scales' one-off layout change happens here, outside any timing
                 sa, sb = quant.preshuffle_e8m0(sa), quant.preshuffle_e8m0(sb)
+            if dtype == "mxfp4km":  # (K/32, M) storage viewed as (M, K/32), as the reference bench does
+                sa, sb = sa.t().contiguous().t(), sb.t().contiguous().t()
             sets.append((pa, pb, sa, sb))
         else:
             raise ValueError(dtype)
@@ -757,16 +766,16 @@ def main():
     dtypes = [d for d in args.dtypes.split(",") if d]
     if args.only:
         dtypes = [args.only]
-    seeds = {"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3, "mxfp4ps": 3}
+    seeds = {"fp16": 1, "bf16": 1, "bf8": 2, "mxfp4": 3, "mxfp4ps": 3, "mxfp4km": 3}
     results = {}
     waves = [int(w) for w in args.waves.split(",") if w]
     cases = [(dt, K, w, REFERENCE_TFLOPS.get(dt) if w == 4 else REFERENCE_TFLOPS_8W.get(dt), args.rotate_mb)
-             for dt in dtypes for w in waves if not (dt == "mxfp4ps" and w == 8)]
+             for dt in dtypes for w in waves if not (dt in FOUR_WAVE_ONLY and w == 8)]
     if args.headline_k and not args.only:
         for dt, (kk, r4, r8) in HEADLINE_K.items():
             if dt in dtypes:
                 cases += [(dt, kk, w, r4 if w == 4 else r8, max(args.rotate_mb, 2048)) for w in waves
-                          if not (dt == "mxfp4ps" and w == 8)]
+                          if not (dt in FOUR_WAVE_ONLY and w == 8)]
     for dt, kk, w, ref, rotate_mb in cases:
         nsets = max(2, -(-rotate_mb * 2**20 // set_bytes(dt, M, N, kk)))
         launch = make_case(dt, M, N, kk, seeds[dt], dev, nsets, w)
@@ -793,9 +802,10 @@ def main():
                 print(f"#   steady state {tel['launch_us']:.1f} us ({tel['tflops']:.0f} TFLOPS) at "
                       f"{tel['power_w']:.0f} W, GFX clock {tel['gfx_clock_mhz']} MHz (amd-smi, {tel['samples']} samples)",
                       flush=True)
-        if args.vendor and not args.only and kk == K and w == 4 and dt in ("fp16", "bf16", "bf8", "mxfp4", "mxfp4ps"):
+        if args.vendor and not args.only and kk == K and w == 4 and dt in ("fp16", "bf16", "bf8", "mxfp4", "mxfp4ps",
+                                                                          "mxfp4km"):
             try:
-                vlaunch = make_vendor_case("mxfp4" if dt == "mxfp4ps" else dt, M, N, kk, seeds[dt], dev, nsets)
+                vlaunch = make_vendor_case("mxfp4" if dt in FOUR_WAVE_ONLY else dt, M, N, kk, seeds[dt], dev, nsets)
             except Exception as e:  # no library kernel for this type on this build
                 results[key]["vendor"] = {"library": "hipBLASLt via torch", "error": str(e).splitlines()[0][:120]}
             else:

@@ -110,5 +110,24 @@ def build(verbose: bool = False, timing: bool = False) -> str:
     return lib_path
 
 
+def resource_table_text(lib_path: str = LIB_PATH) -> str:
+    """The per-kernel register, scratch and LDS table of a built library (from
+    the ``<lib>.resources.json`` build() writes next to it)."""
+    import json
+
+    with open(lib_path + ".resources.json") as fh:
+        rows = json.load(fh)
+    cols = ["agpr", "vgpr_total", "sgpr", "vgpr_spill", "sgpr_spill", "scratch_bytes", "lds_bytes"]
+    heads = ["agpr", "vgpr_total", "sgpr", "vgpr_spill", "sgpr_spill", "scratch_B", "lds_B"]
+    width = max(len(r["kernel"]) for r in rows) + 2
+    out = [f"{'kernel':{width}s}" + " ".join(f"{h:>10s}" for h in heads)]
+    for r in rows:
+        out.append(f"{r['kernel']:{width}s}" + " ".join(f"{r[c]:>10d}" for c in cols))
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv, timing="--timing" in sys.argv))
+    if "--table" in sys.argv:
+        print(resource_table_text(LIB_TIMING_PATH if "--timing" in sys.argv else LIB_PATH))
+    else:
+        print(build(verbose="-v" in sys.argv, timing="--timing" in sys.argv))

@@ -503,6 +503,21 @@ G9_DEV u32 opaque_s(u32 x) {
   asm volatile("" : "+s"(x));
   return x;
 }
+// The thread's index, formed afresh where a tile's set-up starts: the wave's
+// base index is an SGPR (lane 0's threadIdx.x, read once) and the lane comes
+// from mbcnt, so no VGPR holds threadIdx.x for the whole kernel, and the
+// per-lane addresses derived from it are recomputed for every stream-K
+// segment instead of being hoisted out of the persistent loop, where the
+// dozens of them outlived the registers and were spilled.
+// A persistent kernel reads the wave's base once, before its loop, and
+// passes it in as `wb` (threadIdx.x read inside the loop would keep the raw
+// index register alive through it).
+G9_DEV int fresh_tid(int wb = -1) {
+  const int base = wb >= 0 ? wb : __builtin_amdgcn_readfirstlane(threadIdx.x);
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return base + lane;
+}
 
 // SGPR offset of a DMA for a stage past the end of K: the buffer range check
 // covers voffset + soffset + imm, every resource holds at most 2^31 bytes
@@ -580,7 +595,7 @@ struct Pipe {
   int s_end;                // first stage not to load
   u32 kshift;               // GemmParams::kshift
 
-  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int first, int end) {
+  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int first, int end, int wb = -1) {
     // Tile coordinates are wave-uniform; saying so keeps the buffer resources
     // in SGPRs (a resource the compiler thinks divergent is issued through a
     // per-lane "waterfall" loop around every DMA).
@@ -590,7 +605,7 @@ struct Pipe {
     s_end = __builtin_amdgcn_readfirstlane(end);
     kshift = p.kshift;
     lds0 = (u32)(uintptr_t)to_lds(smem);
-    const int tid = threadIdx.x;
+    const int tid = fresh_tid(wb);
     const int lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     mrow = lds0 + (u32)wave * (G::kDmaRows * kRowBytes);
@@ -868,7 +883,7 @@ struct Pipe {
     const rsrc_t r = src(X);
     const u32 soff = stage_off(stage);
     if (stage == 0 && kshift != 0) {
-      const int lane = threadIdx.x & 63;
+      const int lane = fresh_tid(wave << 6) & 63;
       static_for<D>([&](auto J) {
         constexpr int j = decltype(J)::value;
         const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
@@ -1199,11 +1214,11 @@ G9_DEV void tail(const Pipe<OP, G>& P, int s, int n, Acc<G>& acc, ScRegs<OP, G>&
 // complete and the workgroup synchronised, so LDS is free on return.
 template <Op OP, class G>
 G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, Acc<G>& acc,
-                     bool stamp = false) {
+                     bool stamp = false, int wb = -1) {
   using Sh = Shape<OP, G>;
   constexpr bool kScaled = OpInfo<OP>::kScaled;
   Pipe<OP, G> P;
-  P.init(p, smem, tm, tn, s0, s1);
+  P.init(p, smem, tm, tn, s0, s1, wb);
   // Scale chunk 0 (stages s0 .. s0+3) first, then the operands in DMA stream
   // order, per stage A0, B0, B1, A1 (stage s lives in slot (s-s0)&1), with
   // part 0 of chunk 1 where body position 30 would issue it: the prologue
@@ -1305,8 +1320,8 @@ G9_DEV void zero_acc(Acc<G>& acc) {
 // the C write to HBM, and its extra address and swap instructions lengthened
 // it by ~1.5k cycles.
 template <int OUT, class G>
-G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& acc, float scale) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& acc, float scale, int wb = -1) {
+  const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
   const int rr = lane % G::MD, gi = lane / G::MD;
 #pragma unroll
@@ -1496,10 +1511,13 @@ G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
 }
 
 template <Op OP, int OUT, class G>
-G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se, SkTimes& times) {
+G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se, SkTimes& times, int wb) {
   int tm, tn;
-  tile_coords(tile, p.tiles_m * p.tiles_n, p.tiles_m, p.tiles_n, 1, p.group_m, tm, tn);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The grid sizes pass through opaque_s so the divisions are redone per
+  // segment rather than their reciprocals held (in VGPRs) across the loop.
+  const int tiles_m = (int)opaque_s((u32)p.tiles_m), tiles_n = (int)opaque_s((u32)p.tiles_n);
+  tile_coords(tile, tiles_m * tiles_n, tiles_m, tiles_n, 1, (int)opaque_s((u32)p.group_m), tm, tn);
+  const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
   f32x4* ws = reinterpret_cast<f32x4*>(p.ws) + (size_t)tile * (kTile * kTile / 4);
   Acc<G> acc;
   if (sb == 0) {
@@ -1524,9 +1542,9 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
 #endif
   }
   pin_acc<G>(acc);
-  mainloop<OP, G>(p, smem, tm, tn, sb, se, acc);
+  mainloop<OP, G>(p, smem, tm, tn, sb, se, acc, false, wb);
   if (se == p.ns) {
-    store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p));
+    store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p), wb);
     if (sb != 0 && tid == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     [[maybe_unused]] const unsigned long long t3 = clk();
@@ -1571,12 +1589,16 @@ G9_DEV void gemm_sk(const GemmParams& p) {
   long long u1 = u0 + base + (cta < rem ? 1 : 0);
   SkTimes times;
   sk_stamp(0);
+  const int wb = __builtin_amdgcn_readfirstlane(threadIdx.x);
   while (u1 > u0) {
-    const int tile = __builtin_amdgcn_readfirstlane((int)((u1 - 1) / ipt));
+    // ipt through opaque_s: the division is redone per segment, not its
+    // reciprocal held in a VGPR across the loop.
+    const long long ipt_s = (long long)opaque_s((u32)ipt);
+    const int tile = __builtin_amdgcn_readfirstlane((int)((u1 - 1) / ipt_s));
     const long long t0 = (long long)tile * ipt;
     const int sb = __builtin_amdgcn_readfirstlane((int)(max(u0, t0) - t0));
     const int se = __builtin_amdgcn_readfirstlane((int)(u1 - t0));
-    sk_segment<OP, OUT, G>(p, smem, tile, sb, se, times);
+    sk_segment<OP, OUT, G>(p, smem, tile, sb, se, times, wb);
     u1 = t0 + sb;
   }
   sk_stamp(2);
@@ -1597,7 +1619,7 @@ G9_DEV void gemm_sk(const GemmParams& p) {
 // ---------------------------------------------------------------------------
 template <class G>
 G9_DEV void store_partial(const GemmParams& p, float* part, int tm, int tn, Acc<G>& acc) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = fresh_tid(), lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
   const int rr = lane % G::MD, gi = lane / G::MD;
   const size_t np = (size_t)p.tiles_n * kTile;
