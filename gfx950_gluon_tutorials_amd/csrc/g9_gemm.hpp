@@ -117,10 +117,12 @@ G9_DEV void sk_times_store(const SkTimes&) {}
 // to the same MFMAs:
 //   FP4  row-major (M rows of K/32 bytes): each 4-stage scale chunk lands in
 //        LDS as it is in memory and is transposed in place once (see
-//        Pipe::xform_read), after which it has the FP4K layout;
+//        Pipe::xform_read) into the KM layout, 32 rows of all 32 groups per
+//        KiB;
 //   FP4K K-major (K/32 groups of M bytes, the layout of the reference bench's
-//        transposed scale views): the chunk DMA writes the transposed layout
-//        directly;
+//        transposed scale views): the chunk DMA writes the transposed KL
+//        layout directly, 8 groups of all 128 rows of a half tile per KiB, so
+//        each DMA reads whole 128-byte runs;
 //   FP4P preshuffled (quant.preshuffle_e8m0).
 // With 16x16 fragments every layout gives a lane all its scale bytes of a
 // chunk with one LDS read per fragment (ScRegs) and no byte permute.
@@ -271,8 +273,9 @@ template <Op OP>
 constexpr int kMfmaDim8 = OP == Op::FP4 || OP == Op::FP4P ? G9_MD_FP4_8W : kMfmaDim<OP>;
 
 // Scale paths of the scaled kernels:
-//  * kTrScales: chunks in LDS in the transposed ("KM") layout, read with
-//    ds_read_b64_tr_b8 -- FP4 and FP4K with 16x16 fragments and 4 waves;
+//  * kTrScales: chunks in LDS in a transposed layout (KM for FP4, KL for
+//    FP4K), read with ds_read_b64_tr_b8 -- FP4 and FP4K with 16x16
+//    fragments and 4 waves;
 //  * kXform: FP4 of those, whose row-major chunks are transposed in place;
 //  * kChunkScales: a lane reads all its scale bytes of a chunk at once into
 //    ScRegs (kTrScales and FP4P).  The other FP4 kernels (8 waves with 32x32
@@ -693,18 +696,21 @@ struct Pipe {
       msc = lds0 + kScaleBase + (u32)(xw * 128 + r0) * kScRowBytes;
       if constexpr (I::kKMajor) {
         // K-major scales: group q of the operand at q * lds, rows contiguous.
-        // The chunk's KM layout (below) is written directly: lane l of part
-        // j fills group row l / 2 of the part, i.e. group G = 4 (p & 7) +
-        // (p >> 3) of p = l / 2, with the 16 rows 16 ((l & 1) ^ (G & 1)) ..
-        // of the part.  Rows past the operand's end read the next group's
-        // first rows (scales of A or B rows that read zero, whose outputs are
-        // not stored) or, in the last group, zero.
+        // The chunk's KL layout (below) is written directly: lane l of part j
+        // fills unit position l & 7 of group row G = 8 j + l / 8, i.e. the 16
+        // rows 16 u .. of u = (l & 7) ^ (G >> 2), so the eight lanes of a
+        // group row fetch its 128 contiguous bytes and a part reads eight
+        // whole 128-byte runs.  Rows past the operand's end read the next
+        // group's first rows (scales of A or B rows that read zero, whose
+        // outputs are not stored) or, in the last group, zero.
         cstride = __builtin_amdgcn_readfirstlane(lds);
         const u32 groups = (u32)p.K / 32;
         rS = make_rsrc((sa ? p.a_sc : p.b_sc) + hrow, (groups - 1) * lds + (u32)hvalid);
-        const int pr = lane >> 1, grp = 4 * (pr & 7) + (pr >> 3);
 #pragma unroll
-        for (int j = 0; j < SP; ++j) vS[j] = (u32)grp * lds + (u32)(r0 + 32 * j) + 16u * ((lane & 1) ^ (grp & 1));
+        for (int j = 0; j < SP; ++j) {
+          const int grp = 8 * j + (lane >> 3);
+          vS[j] = (u32)grp * lds + 16u * (u32)((lane & 7) ^ (grp >> 2));
+        }
       } else {
         // Row-major scales: lane l of part j fetches the 16-byte half of row
         // 32 j + l / 2 that belongs in its LDS half under the bit-3 row swap.
@@ -717,7 +723,27 @@ struct Pipe {
           vS[j] = (u32)row * lds + half * 16;
         }
       }
-      if constexpr (kTrScales<OP, G>) {
+      if constexpr (I::kKMajor) {
+        // KL layout of a chunk slot (K-major scales): half tile X at X *
+        // 4096, group G (0..31) at + 128 G, the 16-byte unit of its rows
+        // 16 u .. 16 u + 15 at + 16 (u ^ (G >> 2)).  ds_read_b64_tr_b8
+        // gives lane 8a + b of each 16-lane group byte b of the 8-byte units
+        // addressed by lanes a, a + 2, ..., a + 14 of the group (measured on
+        // gfx950).  For fragment F (rows 16 u .. of u = 4 wm + F) lane 16g +
+        // 2k + a addresses the half a of unit (group 4k + g, u), so lane (g,
+        // row rr) receives the scales of its row for groups g, 4 + g, ...,
+        // 28 + g: byte 2 st + h is stage st, MFMA step h, as the MFMAs take
+        // them.  The address of fragment F is fragment 0's with bits 4-5
+        // XORed with F (the unit index is u ^ k and F < 4 only touches its
+        // low bits).  Per 32 lanes (two lane groups: group rows of both
+        // parities, eight unit positions, two halves) the 32 units sit on 64
+        // distinct banks.
+        const int g = lane >> 4, k = (lane >> 1) & 7, a = lane & 1;
+        const u32 off = 128u * (u32)(4 * k + g) + 8u * (u32)a;
+        bS[0][0] = opaque(lds0 + kScaleBase + off + 16u * (u32)((4 * wm) ^ k));
+        bS[1][0] = opaque(lds0 + kScaleBase + 8192u + off + 16u * (u32)((4 * wn) ^ k));
+        sel = 0;
+      } else if constexpr (kTrScales<OP, G>) {
         // KM layout of a chunk slot: half tile X at X * 4096, its part jj
         // (rows 32 jj .. 32 jj + 31) at + jj * 1024; in a part, group G
         // (0..31) is a 32-byte row at position p(G) = (G >> 2) + 8 (G & 3),
@@ -845,7 +871,13 @@ struct Pipe {
   template <int X, int SSLOT, int PAR, int F>
   G9_DEV void read_chunk_scales(ScRegs<OP, G>& sr) const {
     u32x2 v;
-    if constexpr (kTrScales<OP, G>) {
+    if constexpr (I::kKMajor) {
+      u32 base = bS[X >= 2][0];
+      // Formed at the read (inline, so it is not hoisted into a loop-long
+      // register).
+      if constexpr (F != 0) asm volatile("v_xor_b32 %0, %1, %2" : "=v"(base) : "i"(16 * F), "v"(bS[X >= 2][0]));
+      v = tr_read<SSLOT * kScSlotBytes + (X & 1) * 4096>(base);
+    } else if constexpr (kTrScales<OP, G>) {
       v = tr_read<SSLOT * kScSlotBytes + (X & 1) * 4096 + (F / 2) * 1024>(bS[X >= 2][F & 1]);
     } else {
       constexpr int imm = SSLOT * kScSlotBytes + (X & 1) * 128 * kScRowBytes + F * G::MD * kScRowBytes;

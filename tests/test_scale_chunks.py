@@ -7,14 +7,15 @@ group, lane 8a + b receives byte b of the 8-byte units addressed by lanes
 a, a + 2, ..., a + 14 of the group, in that order.
 
 This file restates the kernel's address arithmetic (Pipe::init in
-csrc/g9_gemm.hpp) for the three ways a chunk gets into LDS -- row-major
-scales DMA'd as they are and transposed in place, K-major scales DMA'd
-straight into the transposed layout -- and checks the end result against
-what the MFMAs need, derived independently: lane (g, rr) of fragment F must
-hold, in byte 2 st + h, the scale of its row for MFMA step h of stage st,
-i.e. group 8 st + 4 h + g of the chunk (the K values 32 (8 st + 4 h + g) ..
-of a 16x16x128 fragment's lane group g).  A wrong XOR, a swapped octet, a
-transposed index or an out-of-place write fails at least one check.
+csrc/g9_gemm.hpp) for the two ways a chunk gets into LDS -- row-major scales
+DMA'd as they are and transposed in place into the KM layout, K-major scales
+DMA'd straight into the KL layout in whole 128-byte runs -- and checks the end
+result against what the MFMAs need, derived independently: lane (g, rr) of
+fragment F must hold, in byte 2 st + h, the scale of its row for MFMA step h
+of stage st, i.e. group 8 st + 4 h + g of the chunk (the K values
+32 (8 st + 4 h + g) .. of a 16x16x128 fragment's lane group g).  A wrong XOR,
+a swapped octet, a transposed index or an out-of-place write fails at least
+one check.
 """
 
 import numpy as np
@@ -47,15 +48,22 @@ def dma_row_major(lds, scales, hrow0, xw, ld):
             lds[dst:dst + 16] = src
 
 
+def k_major_dma_sources(j):
+    """(group, first row) fetched by each lane of K-major part DMA j: lane l
+    fills unit position l & 7 of group row G = 8 j + l // 8 with the 16 rows
+    16 u .. of u = (l & 7) ^ (G >> 2)."""
+    out = []
+    for lane in range(64):
+        G = 8 * j + (lane >> 3)
+        out.append((G, 16 * ((lane & 7) ^ (G >> 2))))
+    return out
+
+
 def dma_k_major(lds, scales_km, hrow0, xw):
-    """The K-major chunk DMA of wave xw: lane l of part j fills group row
-    l // 2 of the part, group G = 4 (p & 7) + (p >> 3), with the 16 rows
-    16 ((l & 1) ^ (G & 1)) .. of the part (scales_km is groups x rows)."""
+    """The K-major chunk DMA of wave xw (scales_km is groups x rows): part j
+    writes its lanes' 16-byte units at 1024 j + 16 lane of the wave's 4 KiB."""
     for j in range(4):
-        for lane in range(64):
-            p = lane >> 1
-            G = 4 * (p & 7) + (p >> 3)
-            r = 32 * j + 16 * ((lane & 1) ^ (G & 1))
+        for lane, (G, r) in enumerate(k_major_dma_sources(j)):
             dst = xw * HALF + 1024 * j + 16 * lane
             lds[dst:dst + 16] = scales_km[G, hrow0 + r:hrow0 + r + 16]
 
@@ -99,12 +107,28 @@ def mfma_read(lds, side, wave_col, F):
     return tr_read(lds, addrs), addrs
 
 
-def check_mfma_reads(lds, tile_scales):
+KSCALE_BASE = 131072  # the chunk slots' LDS offset (kScaleBase)
+
+
+def mfma_read_kl(lds, side, wave_col, F):
+    """The K-major kernel's chunk-scale read: bS[X >= 2][0] = kScaleBase +
+    (8192 for B) + 128 (4k + g) + 8a + 16 ((4 wm) ^ k), XORed with 16 F,
+    plus the immediate (X & 1) 4096 -- the kernel's arithmetic on the full
+    address, so a XOR that reached past bits 4-5 would show."""
+    addrs = []
+    for lane in range(64):
+        g, k, a = lane >> 4, (lane >> 1) & 7, lane & 1
+        base = KSCALE_BASE + (8192 if side >= 2 else 0) + 128 * (4 * k + g) + 8 * a + 16 * ((4 * wave_col) ^ k)
+        addrs.append(((base ^ (16 * F)) + (side & 1) * 4096) - KSCALE_BASE)
+    return tr_read(lds, addrs), addrs
+
+
+def check_mfma_reads(lds, tile_scales, read=mfma_read):
     """tile_scales: 512 rows (A then B) x 32 groups of the chunk."""
     for side in range(4):
         for wave_col in range(2):
             for F in range(4):
-                got, _ = mfma_read(lds, side, wave_col, F)
+                got, _ = read(lds, side, wave_col, F)
                 for lane in range(64):
                     g, rr = lane // 16, lane % 16
                     row = 128 * side + 64 * wave_col + 16 * F + rr
@@ -134,10 +158,24 @@ def test_k_major_chunk_feeds_the_mfmas(seed):
     lds = np.zeros(SLOT, dtype=np.uint8)
     for xw in range(4):
         dma_k_major(lds, tile.T.copy(), 128 * xw, xw)
-    check_mfma_reads(lds, tile)
+    check_mfma_reads(lds, tile, read=mfma_read_kl)
 
 
-def test_both_paths_give_the_same_lds_image():
+def test_k_major_parts_fetch_whole_128_byte_runs():
+    # Each part DMA reads eight group rows of 128 contiguous bytes (one
+    # aligned run each for a 128-aligned tile row), and the wave's four
+    # parts write every unit of its 4 KiB once.
+    for j in range(4):
+        src = k_major_dma_sources(j)
+        for G in range(8 * j, 8 * j + 8):
+            rows = sorted(r for g, r in src if g == G)
+            assert rows == list(range(0, 128, 16))
+    units = {(G, r) for j in range(4) for G, r in k_major_dma_sources(j)}
+    assert len(units) == 32 * 8
+
+
+def test_the_row_major_transpose_matches_the_k_major_dma_in_content():
+    # The two layouts differ, but the bytes each MFMA lane receives agree.
     tile = _tile(4)
     a = np.zeros(SLOT, dtype=np.uint8)
     b = np.zeros(SLOT, dtype=np.uint8)
@@ -145,16 +183,37 @@ def test_both_paths_give_the_same_lds_image():
         dma_row_major(a, tile, 128 * xw, xw, 32)
         xform(a, xw)
         dma_k_major(b, tile.T.copy(), 128 * xw, xw)
-    assert np.array_equal(a, b)
+    for side in range(4):
+        for wave_col in range(2):
+            for F in range(4):
+                assert mfma_read(a, side, wave_col, F)[0] == mfma_read_kl(b, side, wave_col, F)[0]
 
 
-def test_a_wrong_octet_swizzle_is_caught():
-    # Plant a mistake in the model of the MFMA read (no XOR on the octet):
-    # the end-to-end check must fail.
+def test_a_wrong_unit_swizzle_is_caught():
+    # Plant a mistake in the model of the K-major read (no XOR of the unit
+    # with k): the end-to-end check must fail.
     tile = _tile(5)
     lds = np.zeros(SLOT, dtype=np.uint8)
     for xw in range(4):
         dma_k_major(lds, tile.T.copy(), 128 * xw, xw)
+    addrs = []
+    for lane in range(64):
+        g, k, a = lane >> 4, (lane >> 1) & 7, lane & 1
+        addrs.append(128 * (4 * k + g) + 8 * a)
+    got = tr_read(lds, addrs)
+    want = [bytes(int(tile[lane % 16, 8 * st + 4 * h + lane // 16]) for st in range(4) for h in range(2))
+            for lane in range(64)]
+    assert got != want
+
+
+def test_a_wrong_octet_swizzle_is_caught():
+    # Plant a mistake in the model of the row-major path's read (no XOR on
+    # the octet): the end-to-end check must fail.
+    tile = _tile(5)
+    lds = np.zeros(SLOT, dtype=np.uint8)
+    for xw in range(4):
+        dma_row_major(lds, tile, 128 * xw, xw, 32)
+        xform(lds, xw)
     addrs = []
     for lane in range(64):
         g, k, a = lane >> 4, (lane >> 1) & 7, lane & 1
@@ -169,14 +228,15 @@ def _banks(addrs, width=8):
     return [((ad // 4) + d) % 64 for ad in addrs for d in range(width // 4)]
 
 
-def test_mfma_reads_are_bank_conflict_free_per_32_lanes():
+@pytest.mark.parametrize("read", [mfma_read, mfma_read_kl])
+def test_mfma_reads_are_bank_conflict_free_per_32_lanes(read):
     # 64 banks x 4 bytes serve 32 lanes of an 8-byte read per cycle: each
     # half wave's units must fall on 64 distinct banks.
     lds = np.zeros(SLOT, dtype=np.uint8)
     for side in range(4):
         for wave_col in range(2):
             for F in range(4):
-                _, addrs = mfma_read(lds, side, wave_col, F)
+                _, addrs = read(lds, side, wave_col, F)
                 for h in range(2):
                     banks = _banks(addrs[32 * h:32 * h + 32])
                     assert len(set(banks)) == 64, (side, wave_col, F, h)
@@ -187,3 +247,4 @@ def test_transpose_reads_are_bank_conflict_free_per_32_lanes():
         addrs = [xform_read_addr(i, lane) for lane in range(64)]
         for h in range(2):
             assert len(set(_banks(addrs[32 * h:32 * h + 32]))) == 64
+
