@@ -515,11 +515,13 @@ G9_DEV u32 opaque_s(u32 x) {
 // A persistent kernel reads the wave's base once, before its loop, and
 // passes it in as `wb` (threadIdx.x read inside the loop would keep the raw
 // index register alive through it).
-G9_DEV int fresh_tid(int wb = -1) {
-  const int base = wb >= 0 ? wb : __builtin_amdgcn_readfirstlane(threadIdx.x);
+G9_DEV int fresh_tid_at(int base) {
   int lane;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
   return base + lane;
+}
+G9_DEV int fresh_tid(int wb = -1) {
+  return fresh_tid_at(wb >= 0 ? wb : __builtin_amdgcn_readfirstlane(threadIdx.x));
 }
 
 // SGPR offset of a DMA for a stage past the end of K: the buffer range check
@@ -915,7 +917,7 @@ struct Pipe {
     const rsrc_t r = src(X);
     const u32 soff = stage_off(stage);
     if (stage == 0 && kshift != 0) {
-      const int lane = fresh_tid(wave << 6) & 63;
+      const int lane = fresh_tid_at(wave << 6) & 63;
       static_for<D>([&](auto J) {
         constexpr int j = decltype(J)::value;
         const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
@@ -1363,15 +1365,23 @@ G9_DEV void store_tile(const GemmParams& p, char* smem, int tm, int tn, Acc<G>& 
 #pragma unroll
       for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < G::FN; ++j)
+        for (int j = 0; j < G::FN; ++j) {
+          // The fragment is copied to VGPRs here, where it is converted:
+          // without the fence the compiler copies the whole tile to VGPRs
+          // ahead of any branch leading here (stream-K: before choosing
+          // between this and the partial store), where the copies outgrow
+          // the registers and spill.
+          accv<G> f = acc[qm][qn][i][j];
+          asm volatile("" : "+v"(f));
           static_for<G::NB>([&](auto B) {
             constexpr int b = decltype(B)::value;
             const int m = qm * 128 + wm * G::FM * G::MD + i * G::MD + rr;
             const int n = qn * 128 + wn * G::FN * G::MD + j * G::MD + 4 * G::NG * b + 4 * gi;
-            const f32x4 v = get_quad<b>(acc[qm][qn][i][j]) * scale;
+            const f32x4 v = get_quad<b>(f) * scale;
             const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
             lds_write8(smem + m * kStageRow + n * 2, h);
           });
+        }
   waitcnt<0, 0>();
   barrier();
   constexpr int kRowsPerPass = G::kThreads / 32;
@@ -1544,17 +1554,22 @@ G9_DEV void wait_flag(const GemmParams& p, int tile, u32 want) {
 
 template <Op OP, int OUT, class G>
 G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se, SkTimes& times, int wb) {
+  // wb is lane 0's threadIdx.x, so the fallback of fresh_tid (which would
+  // keep the raw index register alive through the persistent loop) is dead.
+  __builtin_assume(wb >= 0);
   int tm, tn;
   // The grid sizes pass through opaque_s so the divisions are redone per
   // segment rather than their reciprocals held (in VGPRs) across the loop.
   const int tiles_m = (int)opaque_s((u32)p.tiles_m), tiles_n = (int)opaque_s((u32)p.tiles_n);
   tile_coords(tile, tiles_m * tiles_n, tiles_m, tiles_n, 1, (int)opaque_s((u32)p.group_m), tm, tn);
-  const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
+  // The thread index is formed separately before and after the main loop
+  // (fresh_tid), so no VGPR holds it across the loop.
   f32x4* ws = reinterpret_cast<f32x4*>(p.ws) + (size_t)tile * (kTile * kTile / 4);
   Acc<G> acc;
   if (sb == 0) {
     zero_acc<G>(acc);
   } else {
+    const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
     [[maybe_unused]] const unsigned long long t0 = clk();
     wait_flag(p, tile, (p.epoch << 16) | (u32)sb);
     [[maybe_unused]] const unsigned long long t1 = clk();
@@ -1577,8 +1592,10 @@ G9_DEV void sk_segment(const GemmParams& p, char* smem, int tile, int sb, int se
   mainloop<OP, G>(p, smem, tm, tn, sb, se, acc, false, wb);
   if (se == p.ns) {
     store_tile<OUT, G>(p, smem, tm, tn, acc, epilogue_scale<OP>(p), wb);
-    if (sb != 0 && tid == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sb != 0 && fresh_tid(wb) == 0)
+      __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
+    const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
     [[maybe_unused]] const unsigned long long t3 = clk();
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -1621,7 +1638,9 @@ G9_DEV void gemm_sk(const GemmParams& p) {
   long long u1 = u0 + base + (cta < rem ? 1 : 0);
   SkTimes times;
   sk_stamp(0);
-  const int wb = __builtin_amdgcn_readfirstlane(threadIdx.x);
+  // Through opaque_s, so the compiler keeps the wave base itself rather than
+  // threadIdx.x to re-read it from (a VGPR live through the loop).
+  const int wb = (int)opaque_s((u32)__builtin_amdgcn_readfirstlane(threadIdx.x));
   while (u1 > u0) {
     // ipt through opaque_s: the division is redone per segment, not its
     // reciprocal held in a VGPR across the loop.
