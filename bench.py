@@ -831,17 +831,26 @@ def main():
             launch = make_case("fp16", m, n, k, 4, dev, max(2, -(-args.rotate_mb * 2**20 // set_bytes("fp16", m, n, k))))
             ms_dp = time_case(launch, max(10, args.steps // 2), args.warmup, "dp", args.settle_ms / 2e3)
             ms_sk = time_case(launch, max(10, args.steps // 2), args.warmup, "streamk", args.settle_ms / 2e3)
+            # Stream-K over 256x128 tiles (twice the tiles; bit-identical as well).
+            ms_skh = time_case(launch, max(10, args.steps // 2), args.warmup, "streamk_half", args.settle_ms / 2e3)
             flop = 2.0 * m * n * k
             from gfx950_gluon_tutorials_amd import _lib
 
             tiles, stages = -(-m // 256) * -(-n // 256), k // 64
             ctas = min(tiles * stages, _lib.load().g9_streamk_workgroups())
             fix = streamk_fixups(tiles, stages, ctas)
+            tiles_h = -(-m // 256) * -(-n // 128)
+            ctas_h = min(tiles_h * stages, _lib.load().g9_streamk_workgroups())
+            fix_h = streamk_fixups(tiles_h, stages, ctas_h)
             sk[f"{m}x{n}x{k}"] = {"dp_tflops": round(flop / ms_dp / 1e9, 2), "sk_tflops": round(flop / ms_sk / 1e9, 2),
-                                  "dp_ms": round(ms_dp, 5), "sk_ms": round(ms_sk, 5), "sk_workgroups": ctas,
-                                  "fixups": fix, "fixup_bytes": fix * 2 * 256 * 256 * 4}
-            print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f} TFLOPS  "
-                  f"({ctas} workgroups, {fix} partial-tile handoffs = {fix * 0.5:.0f} MiB fp32 written+read)",
+                                  "sk_half_tflops": round(flop / ms_skh / 1e9, 2),
+                                  "dp_ms": round(ms_dp, 5), "sk_ms": round(ms_sk, 5), "sk_half_ms": round(ms_skh, 5),
+                                  "sk_workgroups": ctas, "fixups": fix, "fixup_bytes": fix * 2 * 256 * 256 * 4,
+                                  "sk_half_tiles": tiles_h, "sk_half_fixups": fix_h,
+                                  "sk_half_fixup_bytes": fix_h * 2 * 256 * 128 * 4}
+            print(f"# stream-K {m}x{n}x{k}: dp {flop / ms_dp / 1e9:.1f}  sk {flop / ms_sk / 1e9:.1f}  "
+                  f"sk 256x128 {flop / ms_skh / 1e9:.1f} TFLOPS  ({ctas} workgroups, {fix} partial-tile handoffs = "
+                  f"{fix * 0.5:.0f} MiB fp32 written+read; 256x128: {tiles_h} tiles, {fix_h} handoffs)",
                   flush=True)
             del launch
             torch.cuda.empty_cache()

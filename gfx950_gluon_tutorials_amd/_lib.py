@@ -40,9 +40,11 @@ G9_FP4K = 5  # MXFP4 with K-major scales (g9_gemm_a4w4 given K-major scale views
 G9_SCHED_DP = 0
 G9_SCHED_SK = 1
 G9_SCHED_SPLITK = 2
+G9_SCHED_SK_HALF = 3  # stream-K over 256x128 tiles (a16w16, 4 waves)
 
 SCHEDULES = {"dp": G9_SCHED_DP, "data_parallel": G9_SCHED_DP, "sk": G9_SCHED_SK, "streamk": G9_SCHED_SK,
-             "splitk": G9_SCHED_SPLITK, "split_k": G9_SCHED_SPLITK}
+             "splitk": G9_SCHED_SPLITK, "split_k": G9_SCHED_SPLITK, "streamk_half": G9_SCHED_SK_HALF,
+             "sk_half": G9_SCHED_SK_HALF}
 
 # Exported symbols and their signatures; the CPU test checks the library
 # exports exactly these.

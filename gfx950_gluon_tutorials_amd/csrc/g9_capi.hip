@@ -38,6 +38,15 @@ G9_DEFINE(g9_a8w8_bf16out, Op::BF8, OUT_BF16)
 G9_DEFINE(g9_a4w4_bf16out, Op::FP4, OUT_BF16)
 G9_DEFINE(g9_a4w4_f16out, Op::FP4, OUT_F16)
 
+// Stream-K over 256x128 tiles (FP16/BF16, 4-wave).
+using G9Half4 = Geo4<16>;
+extern "C" __global__ G9_ATTRS(G9Half4) void g9_a16w16_f16_skh_4w(GemmParams p) {
+  gemm_sk_h<Op::F16, OUT_F16, G9Half4>(p);
+}
+extern "C" __global__ G9_ATTRS(G9Half4) void g9_a16w16_bf16_skh_4w(GemmParams p) {
+  gemm_sk_h<Op::BF16, OUT_BF16, G9Half4>(p);
+}
+
 // MXFP4 with preshuffled scales: data-parallel, 4-wave.
 using G9Fp4p4 = Geo4<kMfmaDim<Op::FP4P>>;
 extern "C" __global__ G9_ATTRS(G9Fp4p4) void g9_a4w4ps_bf16out_dp_4w(GemmParams p) {
@@ -122,6 +131,8 @@ const KernelEntry kKernels[] = {
     {G9_FP4K, G9_F16, G9_SCHED_DP, 4, g9_a4w4km_f16out_dp_4w, "g9_a4w4km_f16out_dp_4w"},
     {G9_FP4K, G9_BF16, G9_SCHED_SK, 4, g9_a4w4km_bf16out_sk_4w, "g9_a4w4km_bf16out_sk_4w"},
     {G9_FP4K, G9_F16, G9_SCHED_SK, 4, g9_a4w4km_f16out_sk_4w, "g9_a4w4km_f16out_sk_4w"},
+    {G9_F16, G9_F16, G9_SCHED_SK_HALF, 4, g9_a16w16_f16_skh_4w, "g9_a16w16_f16_skh_4w"},
+    {G9_BF16, G9_BF16, G9_SCHED_SK_HALF, 4, g9_a16w16_bf16_skh_4w, "g9_a16w16_bf16_skh_4w"},
 };
 
 #define G9_SPLITK_ENTRY(DT, OUT, NAME)                                                              \
@@ -180,6 +191,9 @@ constexpr int kNumXcds = 8;
 constexpr int kGroupM = 4;
 constexpr size_t kWsHeader = 256;          // error word + padding
 constexpr size_t kWsTileBytes = 256 * 256 * 4;
+// Workspaces are accounted in units of a 256x128 tile's fp32 partial: a
+// 256x256 partial is two, and the flag region holds one flag per unit.
+constexpr size_t kWsUnit = kWsTileBytes / 2;
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -211,27 +225,35 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // of any stream-K launch that fits it), then the partials.  Split-K never
 // writes the header or the flags, so one workspace serves both schedules.
 size_t splitk_base(size_t ws_bytes) {
-  return kWsHeader + flags_bytes((long long)((ws_bytes - kWsHeader) / kWsTileBytes + 1));
+  return kWsHeader + flags_bytes((long long)((ws_bytes - kWsHeader) / kWsUnit + 1));
 }
 // Smallest workspace whose partials (behind its own flag region) hold
-// `partials` tiles.  Stream-K needs one partial (and one flag) per tile.
-size_t splitk_bytes(long long partials) {
-  size_t s = kWsHeader + flags_bytes(partials + 1) + (size_t)partials * kWsTileBytes;
-  while (splitk_base(s) + (size_t)partials * kWsTileBytes > s) s += 256;
+// `units` partial units.  Stream-K needs one partial (and one flag) per tile.
+size_t units_bytes(long long units) {
+  size_t s = kWsHeader + flags_bytes(units + 1) + (size_t)units * kWsUnit;
+  while (splitk_base(s) + (size_t)units * kWsUnit > s) s += 256;
   return s;
 }
-size_t streamk_bytes(long long tiles) { return splitk_bytes(tiles); }
+size_t splitk_bytes(long long partials) { return units_bytes(2 * partials); }
+size_t streamk_bytes(long long tiles) { return units_bytes(2 * tiles); }
+size_t streamk_half_bytes(long long tiles) { return units_bytes(tiles); }
 
 // Shared launch path.  Sizes/strides were validated by the caller except the
 // generic checks done here.
 int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
            void* stream) {
   if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
-  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK) return G9_ERR_SCHEDULE;
+  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK &&
+      schedule != G9_SCHED_SK_HALF)
+    return G9_ERR_SCHEDULE;
+  // 256x128 stream-K tiles exist for FP16/BF16 with 4 waves only.
+  if (schedule == G9_SCHED_SK_HALF && (waves != 4 || (dtype != G9_F16 && dtype != G9_BF16)))
+    return G9_ERR_SCHEDULE;
   const KernelEntry* k = find_kernel(dtype, out, schedule, waves);
   if (!k) return G9_ERR_DTYPE;
+  const bool half = schedule == G9_SCHED_SK_HALF;
   p.tiles_m = (p.M + kTile - 1) / kTile;
-  p.tiles_n = (p.N + kTile - 1) / kTile;
+  p.tiles_n = half ? (p.N + 127) / 128 : (p.N + kTile - 1) / kTile;
   p.num_xcds = kNumXcds;
   p.group_m = kGroupM;
   const long long tiles = (long long)p.tiles_m * p.tiles_n;
@@ -268,9 +290,11 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     // The partials go behind the whole flag region g9_workspace_init clears
     // for this workspace size (as split-K's do), so a launch with fewer tiles
     // never writes partials over flag words a later, larger launch polls.
-    if (!ws || ws_bytes < streamk_bytes(tiles) || !aligned(ws, 256)) return G9_ERR_WORKSPACE;
+    const size_t tile_bytes = half ? kWsUnit : kWsTileBytes;
+    if (!ws || ws_bytes < (half ? streamk_half_bytes(tiles) : streamk_bytes(tiles)) || !aligned(ws, 256))
+      return G9_ERR_WORKSPACE;
     const size_t base = splitk_base(ws_bytes);
-    if (base + (size_t)tiles * kWsTileBytes > ws_bytes) return G9_ERR_WORKSPACE;
+    if (base + (size_t)tiles * tile_bytes > ws_bytes) return G9_ERR_WORKSPACE;
     char* w = static_cast<char*>(ws);
     p.err = reinterpret_cast<int*>(w);
     p.flags = reinterpret_cast<u32*>(w + kWsHeader);
@@ -611,6 +635,7 @@ size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedul
     const int S = cus > 0 ? g9_splitk_factor(tiles, (int)((K + stage_k(dtype) - 1) / stage_k(dtype)), cus) : 1;
     return S > 1 ? splitk_bytes(tiles * S) : 0;
   }
+  if (schedule == G9_SCHED_SK_HALF) return streamk_half_bytes(((M + kTile - 1) / kTile) * ((N + 127) / 128));
   if (schedule != G9_SCHED_SK) return 0;
   return streamk_bytes(tiles);
 }
@@ -657,7 +682,7 @@ int g9_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   // Header and flags precede the partial tiles.  Clear the flags of the
   // largest tile count whose partials fit this workspace, so every launch the
   // workspace is large enough for finds its flags cleared.
-  const size_t max_tiles = (workspace_bytes - kWsHeader) / kWsTileBytes + 1;
+  const size_t max_tiles = (workspace_bytes - kWsHeader) / kWsUnit + 1;
   size_t words = (kWsHeader + flags_bytes((long long)max_tiles)) / 4;
   if (words > workspace_bytes / 4) words = workspace_bytes / 4;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -734,7 +759,8 @@ int g9_streamk_workgroups(void) { return cu_count(); }
 // ---------------------------------------------------------------------------
 // Allocation-free a16w16 (g9_gemm_a16w16_noalloc): the stream-K / split-K
 // workspace is this static device array instead of a caller buffer.  It holds
-// kScratchTiles partial tiles (64 MiB plus the header and flag words) and
+// kScratchTiles 256x256 partial tiles, or twice as many 256x128 ones (64 MiB
+// plus the header and one flag word per 256x128 unit), and
 // lives, on every GPU the library runs on, until the process ends.  Host code
 // never passes `scratch` itself to a kernel (in host code the name is a
 // stand-in, not a device address): the device address comes from
@@ -742,7 +768,7 @@ int g9_streamk_workgroups(void) { return cu_count(); }
 // ---------------------------------------------------------------------------
 constexpr long long kScratchTiles = G9_NOALLOC_MAX_TILES;
 constexpr size_t kScratchBytes =
-    kWsHeader + ((size_t)(kScratchTiles + 1) * 4 + 255) / 256 * 256 + (size_t)kScratchTiles * kWsTileBytes;
+    kWsHeader + ((size_t)(2 * kScratchTiles + 1) * 4 + 255) / 256 * 256 + (size_t)kScratchTiles * kWsTileBytes;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -789,7 +815,10 @@ int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int
   int st = prep_a16w16(p, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn, dtype);
   if (st) return st;
   if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
-  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK) return G9_ERR_SCHEDULE;
+  if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK &&
+      schedule != G9_SCHED_SK_HALF)
+    return G9_ERR_SCHEDULE;
+  if (schedule == G9_SCHED_SK_HALF && waves != 4) return G9_ERR_SCHEDULE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int dev = 0;
   if (hipStreamGetDevice(s, &dev) != hipSuccess) return G9_ERR_HIP;
@@ -803,7 +832,8 @@ int g9_gemm_a16w16_noalloc(const void* a, const void* b, void* c, int64_t M, int
   // Stream-K needs its error word and flags at zero: clear them with a fill
   // kernel (no hipMemsetAsync, so the call can be captured in a graph).
   // Split-K writes every partial it reads, so it needs no clearing.
-  if (schedule == G9_SCHED_SK && (st = g9_workspace_init(ws, kScratchBytes, stream))) return st;
+  if ((schedule == G9_SCHED_SK || schedule == G9_SCHED_SK_HALF) && (st = g9_workspace_init(ws, kScratchBytes, stream)))
+    return st;
   return launch(dtype, dtype, schedule, waves, p, ws, kScratchBytes, stream);
 }
 

@@ -1657,6 +1657,401 @@ G9_DEV void gemm_sk(const GemmParams& p) {
 }
 
 // ---------------------------------------------------------------------------
+// Stream-K with 256x128 tiles (FP16/BF16, 4 waves).
+//
+// The BASELINE stream-K shapes have fewer 256x256 tiles than CUs (225 and
+// 160), where a bit-identical stream-K cannot beat data-parallel: each
+// element's K chain is serial, so no range can be shorter than one tile
+// chain.  Tiles of 256x128 double the count (450 and 320) so every range
+// spans more than a tile.  The tile is two quadrants, A0 x B0 and A1 x B0,
+// each computed by the four waves exactly as a 256x256 tile's quadrant (the
+// same fragments, snake order and MFMA steps), so every output element sees
+// the data-parallel kernel's MFMA sequence and the result is bit-identical to
+// it.  Per K stage the tile needs the A0, A1 and B0 sub-buffers (48 KiB):
+// three stages are resident (144 KiB), so a stage's DMAs are issued three
+// stages ahead.  A stage is two regions of 32 MFMAs per wave:
+//   R0: A0 x B0;  reads A1 of this stage and B0 fragments 0-1 of the next;
+//       DMAs B0 and half of A0 of the stage three ahead (6 per wave)
+//   R1: A1 x B0;  reads A0 of the next stage and B0 fragments 2-3;
+//       DMAs the other half of A0 and A1 of the stage three ahead
+// Each region waits for its wave's DMAs of three regions earlier (the data it
+// reads was issued at least four regions before), then passes the region
+// barrier: every wave's reads of the sub-buffers refilled now ended before
+// it.  The B registers alternate by stage parity and the slots cycle by 3, so
+// the loop body is six stages.  Against the 256x256 tile it issues 1.5x the
+// DMAs and LDS reads per MFMA.
+// ---------------------------------------------------------------------------
+constexpr int kHnTileN = 128;
+constexpr int kHnSlots = 3;
+// LDS byte offset of sub-buffer X (0: A0, 1: A1, 2: B0) in slot s.
+constexpr int hn_off(int X, int s) { return (X * kHnSlots + s) * kSubBytes; }
+constexpr int kHnLdsBytes = 3 * kHnSlots * kSubBytes;  // 144 KiB
+constexpr int kHnStageRow = kHnTileN * 2 + 16;         // epilogue staging pitch (bytes)
+static_assert(kTile * kHnStageRow <= kHnLdsBytes, "staging must fit");
+static_assert(hn_off(2, kHnSlots - 1) + kSubBytes <= 65536 * 3, "LDS layout");
+
+template <class G>
+using AccH = accv<G>[2][G::FM][G::FN];  // [A half][i][j]
+
+template <Op OP, class G>
+struct PipeH {
+  static_assert(OP == Op::F16 || OP == Op::BF16, "256x128 stream-K tiles are FP16/BF16");
+  static_assert(G::NW == 4 && G::MD == 16, "256x128 stream-K tiles run 4 waves of 16x16 fragments");
+  static constexpr int D = G::kDmaPerSub;
+  rsrc_t rA[2], rB;
+  u32 vA[D], vB[D];
+  u32 bA0[G::NC], bA1[G::NC], bB[G::NC];
+  u32 lds0, mrow;
+  int wave, s_end;
+  u32 kshift;
+
+  G9_DEV void init(const GemmParams& p, char* smem, int tm, int tn, int end, int wb) {
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
+    s_end = __builtin_amdgcn_readfirstlane(end);
+    kshift = p.kshift;
+    lds0 = (u32)(uintptr_t)to_lds(smem);
+    const int tid = fresh_tid(wb);
+    const int lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    mrow = lds0 + (u32)wave * (G::kDmaRows * kRowBytes);
+    const int wm = wave / G::WN, wn = wave % G::WN;
+    const int gi = lane / G::MD, rr = lane % G::MD;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ra = tm * kTile + h * 128;
+      const int va = __builtin_amdgcn_readfirstlane(min(max(p.M - ra, 0), 128));
+      rA[h] = make_rsrc(p.a + (size_t)ra * p.lda - p.kshift, (u32)va * p.lda + p.kshift);
+    }
+    const int rb = tn * kHnTileN;
+    const int vb = __builtin_amdgcn_readfirstlane(min(max(p.N - rb, 0), 128));
+    rB = make_rsrc(p.b + (size_t)rb * p.ldb - p.kshift, (u32)vb * p.ldb + p.kshift);
+    // The 256x256 kernel's DMA offsets and row swizzle (Pipe::init).
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
+      const int ch = (lane & 7) ^ ((row >> 1) & 7);
+      vA[j] = (u32)row * p.lda + ch * 16 - 1024u * j;
+      vB[j] = (u32)row * p.ldb + ch * 16 - 1024u * j;
+    }
+    const int sw = (rr >> 1) & 7;
+#pragma unroll
+    for (int c = 0; c < G::NC; ++c) {
+      const int slot = G::chunk(c, gi) ^ sw;
+      const u32 ra = (u32)(wm * G::FM * G::MD + rr) * kRowBytes + slot * 16;
+      bA0[c] = opaque(lds0 + hn_off(0, 0) + ra);
+      bA1[c] = opaque(lds0 + hn_off(1, 0) + ra);
+      bB[c] = opaque(lds0 + hn_off(2, 0) + (u32)(wn * G::FN * G::MD + rr) * kRowBytes + slot * 16);
+    }
+  }
+  G9_DEV rsrc_t src(int X) const { return X == 0 ? rA[0] : X == 1 ? rA[1] : rB; }
+  G9_DEV u32 stage_off(int stage) const { return stage < s_end ? (u32)stage * kRowBytes : kDeadOff; }
+  // 16-byte LDS read number R (fragment R / NC, chunk R % NC) of sub-buffer X.
+  template <int X, int SLOT, int R>
+  G9_DEV void read_chunk(FragSet<G>& f) const {
+    constexpr int NC = G::NC;
+    constexpr int imm = SLOT * kSubBytes + (R / NC) * G::MD * kRowBytes;
+    static_assert(imm < 65536, "DS offsets are 16 bits");
+    const u32 base = X == 0 ? bA0[R % NC] : X == 1 ? bA1[R % NC] : bB[R % NC];
+    f[R / NC].c[R % NC] = *(const G9_LDS u32x4*)(uintptr_t)(base + imm);
+  }
+  template <int X, int SLOT, int J>
+  G9_DEV void dma_rows(rsrc_t r, u32 soff, u32 mb) const {
+    dma16<J * 1024>(r, (G9_LDS void*)(uintptr_t)(mb + hn_off(X, SLOT)), X < 2 ? vA[J] : vB[J], soff);
+  }
+  // Every DMA of sub-buffer X for `stage` (the prologue), with the K-tail
+  // handling of Pipe::issue.
+  template <int X, int SLOT>
+  G9_DEV void issue(int stage) const {
+    const rsrc_t r = src(X);
+    const u32 soff = stage_off(stage);
+    if (stage == 0 && kshift != 0) {
+      const int lane = fresh_tid_at(wave << 6) & 63;
+      static_for<D>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int row = G::kDmaRows * wave + 8 * j + (lane >> 3);
+        const int ch = (lane & 7) ^ ((row >> 1) & 7);
+        const u32 v = (u32)ch * 16 < kshift ? kDeadOff : (X < 2 ? vA[j] : vB[j]);
+        dma16<j * 1024>(r, (G9_LDS void*)(uintptr_t)(mrow + hn_off(X, SLOT)), v, soff);
+      });
+      return;
+    }
+    static_for<D>([&](auto J) { dma_rows<X, SLOT, decltype(J)::value>(r, soff, mrow); });
+  }
+  template <int X, int SLOT>
+  G9_DEV void load(FragSet<G>& f) const {
+    constexpr int NF = X < 2 ? G::FM : G::FN;
+    static_for<G::NC * NF>([&](auto R) { read_chunk<X, SLOT, decltype(R)::value>(f); });
+  }
+};
+
+// Region slots of the 256x128 tile: 2 MFMAs before the barrier, the 12 reads
+// over the next 15 MFMA slots, the 6 DMAs spread over the region.
+struct SlotsH {
+  static constexpr int NM = 32, kPre = 2, NQ = NM - kPre, NR = 12, ND = 6;
+  static constexpr int read_q(int R) { return R * 15 / NR; }
+  static constexpr int dma_q(int J) { return 1 + J * (NQ - 1) / ND; }
+};
+constexpr int kHnVmWait = 3 * SlotsH::ND;  // DMAs of the three previous regions
+
+// One region: MFMAs of quadrant acc (B fragments bx, A fragments ay); reads of
+// A sub-buffer XA / slot SA into na and of B fragments FB0, FB0 + 1 of slot
+// SB into nb; DMAs (DPOS 0: B0 and A0 rows 0-15 of the wave's, DPOS 1: A0 rows
+// 16-31 and A1) of stage ds into slot SD.
+template <Op OP, class G, int XA, int SA, int SB, int FB0, int DPOS, int SD>
+G9_DEV void region_h(const PipeH<OP, G>& P, int ds, QAcc<G>& acc, const FragSet<G>& bx, const FragSet<G>& ay,
+                     FragSet<G>& na, FragSet<G>& nb) {
+  using S = SlotsH;
+  static_assert(G::FM * G::NC == 8 && G::NC == 2, "the read table assumes 4 A fragments of 2 chunks");
+  __builtin_amdgcn_sched_barrier(0);
+  waitcnt<kHnVmWait, 0>();
+  const u32 soff = P.stage_off(ds);
+  const u32 mb = opaque_s(P.mrow);
+  auto slot = [&](auto KC) {
+    constexpr int K = decltype(KC)::value;
+    constexpr int e = K / (G::FM * G::FN), i = (K / G::FN) % G::FM, j0 = K % G::FN;
+    constexpr int j = (i % 2) ? G::FN - 1 - j0 : j0;
+    mma<OP, G, e>(acc[i][j], bx[j], ay[i]);
+    constexpr int q = K - S::kPre;
+    if constexpr (q >= 0) {
+      static_for<S::NR>([&](auto RC) {
+        constexpr int R = decltype(RC)::value;
+        if constexpr (S::read_q(R) == q) {
+          if constexpr (R < 8)
+            P.template read_chunk<XA, SA, R>(na);
+          else
+            P.template read_chunk<2, SB, FB0 * G::NC + (R - 8)>(nb);
+        }
+      });
+      static_for<S::ND>([&](auto JC) {
+        constexpr int J = decltype(JC)::value;
+        if constexpr (S::dma_q(J) == q) {
+          constexpr int X = DPOS == 0 ? (J < 4 ? 2 : 0) : (J < 2 ? 0 : 1);
+          constexpr int jj = DPOS == 0 ? (J < 4 ? J : J - 4) : (J < 2 ? J + 2 : J - 2);
+          P.template dma_rows<X, SD, jj>(P.src(X), soff, mb);
+        }
+      });
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_for<S::kPre>([&](auto K) { slot(K); });
+  barrier();
+  static_for<S::NM - S::kPre>([&](auto K) { slot(std::integral_constant<int, decltype(K)::value + S::kPre>{}); });
+}
+
+template <bool A, class T>
+G9_DEV T& pick(T& x, T& y) {
+  if constexpr (A)
+    return x;
+  else
+    return y;
+}
+
+// Stage K (0..5) of the six-stage body starting at stage s.
+template <Op OP, class G, int K>
+G9_DEV void stage_h(const PipeH<OP, G>& P, int s, AccH<G>& acc, FragSet<G>& at, FragSet<G>& ab, FragSet<G>& x,
+                    FragSet<G>& y) {
+  constexpr int sg = K % kHnSlots, sn = (K + 1) % kHnSlots;
+  FragSet<G>& bx = pick<K % 2 == 0>(x, y);
+  FragSet<G>& nb = pick<K % 2 == 0>(y, x);
+  const int ds = s + K + kHnSlots;
+  region_h<OP, G, 1, sg, sn, 0, 0, sg>(P, ds, acc[0], bx, at, ab, nb);
+  region_h<OP, G, 0, sn, sn, 2, 1, sg>(P, ds, acc[1], bx, ab, at, nb);
+}
+
+template <Op OP, class G, int K>
+G9_DEV void tail_h(const PipeH<OP, G>& P, int s, int n, AccH<G>& acc, FragSet<G>& at, FragSet<G>& ab,
+                   FragSet<G>& x, FragSet<G>& y) {
+  if constexpr (K + 1 < 2 * kHnSlots) {
+    if (n > K) {
+      stage_h<OP, G, K>(P, s, acc, at, ab, x, y);
+      tail_h<OP, G, K + 1>(P, s, n, acc, at, ab, x, y);
+    }
+  }
+}
+
+template <class G>
+G9_DEV void pin_acc_h(AccH<G>& acc) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FN; ++j) asm volatile("" : "+a"(acc[q][i][j]));
+}
+template <class G>
+G9_DEV void settle_acc_h(AccH<G>& acc) {
+  mfma_drain();
+  pin_acc_h<G>(acc);
+}
+
+// Accumulates stages [s0, s1) of 256x128 tile (tm, tn) into acc; leaves every
+// DMA complete and the workgroup synchronised.
+template <Op OP, class G>
+G9_DEV void mainloop_h(const GemmParams& p, char* smem, int tm, int tn, int s0, int s1, AccH<G>& acc, int wb) {
+  constexpr int D = G::kDmaPerSub;
+  PipeH<OP, G> P;
+  P.init(p, smem, tm, tn, s1, wb);
+  // Stages s0 .. s0 + 2 into slots 0 .. 2, each B0, A0, A1 (the order the
+  // loop issues them in), then stage s0's B0 and A0 are read.
+  P.template issue<2, 0>(s0);
+  P.template issue<0, 0>(s0);
+  P.template issue<1, 0>(s0);
+  P.template issue<2, 1>(s0 + 1);
+  P.template issue<0, 1>(s0 + 1);
+  P.template issue<1, 1>(s0 + 1);
+  P.template issue<2, 2>(s0 + 2);
+  P.template issue<0, 2>(s0 + 2);
+  P.template issue<1, 2>(s0 + 2);
+  waitcnt<7 * D, 0>();
+  barrier();
+  FragSet<G> at, ab, x, y;
+  P.template load<0, 0>(at);
+  P.template load<2, 0>(x);
+  mfma_drain();
+  int s = s0;
+  for (; s + 2 * kHnSlots <= s1; s += 2 * kHnSlots)
+    static_for<2 * kHnSlots>([&](auto K) { stage_h<OP, G, decltype(K)::value>(P, s, acc, at, ab, x, y); });
+  settle_acc_h<G>(acc);
+  if (s < s1) {
+    tail_h<OP, G, 0>(P, s, s1 - s, acc, at, ab, x, y);
+    settle_acc_h<G>(acc);
+  }
+  waitcnt<0, 0>();
+  barrier();
+}
+
+// store_tile for a 256x128 tile (staging pitch kHnStageRow).
+template <int OUT, class G>
+G9_DEV void store_tile_h(const GemmParams& p, char* smem, int tm, int tn, AccH<G>& acc, int wb) {
+  const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  const int rr = lane % G::MD, gi = lane / G::MD;
+#pragma unroll
+  for (int qm = 0; qm < 2; ++qm)
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FN; ++j) {
+        accv<G> f = acc[qm][i][j];
+        asm volatile("" : "+v"(f));
+        static_for<G::NB>([&](auto B) {
+          constexpr int b = decltype(B)::value;
+          const int m = qm * 128 + wm * G::FM * G::MD + i * G::MD + rr;
+          const int n = wn * G::FN * G::MD + j * G::MD + 4 * G::NG * b + 4 * gi;
+          const f32x4 v = get_quad<b>(f);
+          const u32x2 h = OUT == OUT_BF16 ? pack4_bf16(v) : pack4_f16(v);
+          lds_write8(smem + m * kHnStageRow + n * 2, h);
+        });
+      }
+  waitcnt<0, 0>();
+  barrier();
+  constexpr int kChunks = kHnTileN / 8;  // 16-byte chunks per row
+  constexpr int kRowsPerPass = G::kThreads / kChunks;
+  const int ch = tid % kChunks;
+  const int row0 = tm * kTile, col = tn * kHnTileN + ch * 8;
+  char* cbase = p.c + (size_t)col * 2;
+#pragma unroll 4
+  for (int pass = 0; pass < kTile / kRowsPerPass; ++pass) {
+    const int r = pass * kRowsPerPass + tid / kChunks;
+    const u32x4 d = lds_read16(smem + r * kHnStageRow + ch * 16);
+    const int m = row0 + r;
+    if (m < p.M) {
+      char* dst = cbase + (size_t)m * p.ldc * 2;
+      if (col + 8 <= p.N && ((uintptr_t)dst & 15) == 0) {
+        __builtin_nontemporal_store(d, reinterpret_cast<u32x4*>(dst));
+      } else {
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&d);
+        for (int e = 0; e < 8; ++e)
+          if (col + e < p.N) reinterpret_cast<uint16_t*>(dst)[e] = hv[e];
+      }
+    }
+  }
+  barrier();
+}
+
+// Index (in f32x4) of a wave's fragment in a 256x128 tile's partial.
+template <class G>
+G9_DEV int ws_index_h(int wave, int q, int i, int j, int lane) {
+  return ((wave * (2 * G::FM * G::FN) + (q * G::FM + i) * G::FN + j) * 64 + lane);
+}
+
+template <Op OP, int OUT, class G>
+G9_DEV void sk_segment_h(const GemmParams& p, char* smem, int tile, int sb, int se, int wb) {
+  __builtin_assume(wb >= 0);
+  int tm, tn;
+  const int tiles_m = (int)opaque_s((u32)p.tiles_m), tiles_n = (int)opaque_s((u32)p.tiles_n);
+  tile_coords(tile, tiles_m * tiles_n, tiles_m, tiles_n, 1, (int)opaque_s((u32)p.group_m), tm, tn);
+  f32x4* ws = reinterpret_cast<f32x4*>(p.ws) + (size_t)tile * (kTile * kHnTileN / 4);
+  AccH<G> acc;
+  if (sb == 0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::FN; ++j) acc[q][i][j] = accv<G>{};
+  } else {
+    const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
+    wait_flag(p, tile, (p.epoch << 16) | (u32)sb);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::FN; ++j) acc[q][i][j] = ws[ws_index_h<G>(wave, q, i, j, lane)];
+  }
+  pin_acc_h<G>(acc);
+  mainloop_h<OP, G>(p, smem, tm, tn, sb, se, acc, wb);
+  if (se == p.ns) {
+    store_tile_h<OUT, G>(p, smem, tm, tn, acc, wb);
+    if (sb != 0 && fresh_tid(wb) == 0)
+      __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    const int tid = fresh_tid(wb), lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::FN; ++j) ws[ws_index_h<G>(wave, q, i, j, lane)] = acc[q][i][j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    barrier();
+    if (tid == 0)
+      __hip_atomic_store(p.flags + tile, (p.epoch << 16) | (u32)se, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The stream-K schedule of gemm_sk over 256x128 tiles (p.tiles_n counts
+// 128-column tiles).
+template <Op OP, int OUT, class G>
+G9_DEV void gemm_sk_h(const GemmParams& p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kHnLdsBytes];
+  const int G_ = p.sk_ctas;
+  int cta = blockIdx.x;
+  {
+    int cm, cn;
+    tile_coords(cta, G_, G_, 1, p.num_xcds, 1, cm, cn);
+    cta = cm;
+  }
+  const long long ipt = p.ns;
+  const long long total = (long long)p.tiles_m * p.tiles_n * ipt;
+  const long long base = total / G_, rem = total % G_;
+  const long long u0 = cta * base + min((long long)cta, rem);
+  long long u1 = u0 + base + (cta < rem ? 1 : 0);
+  const int wb = (int)opaque_s((u32)__builtin_amdgcn_readfirstlane(threadIdx.x));
+  while (u1 > u0) {
+    const long long ipt_s = (long long)opaque_s((u32)ipt);
+    const int tile = __builtin_amdgcn_readfirstlane((int)((u1 - 1) / ipt_s));
+    const long long t0 = (long long)tile * ipt;
+    const int sb = __builtin_amdgcn_readfirstlane((int)(max(u0, t0) - t0));
+    const int se = __builtin_amdgcn_readfirstlane((int)(u1 - t0));
+    sk_segment_h<OP, OUT, G>(p, smem, tile, sb, se, wb);
+    u1 = t0 + sb;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Split-K schedule, for grids with too few tiles to fill the chip.
 //
 // Each tile's K stages are cut into `split` contiguous segments of near-equal

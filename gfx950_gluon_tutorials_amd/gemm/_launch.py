@@ -59,7 +59,8 @@ def _schedule_code(schedule, M: int, N: int, dtype: int) -> int:
     try:
         return _lib.SCHEDULES[name]
     except KeyError:
-        raise ValueError(f"unknown schedule {schedule!r} (expected 'dp', 'streamk', 'splitk' or 'auto')") from None
+        raise ValueError(f"unknown schedule {schedule!r} (expected 'dp', 'streamk', 'streamk_half', 'splitk' or "
+                         "'auto')") from None
 
 
 def _require_device(*tensors: torch.Tensor) -> torch.device:
@@ -200,15 +201,18 @@ WORKSPACES = _Workspaces()
 CHECK_STREAMK = os.environ.get("G9_CHECK", "0") not in ("", "0")
 
 
+_STREAMK = (_lib.G9_SCHED_SK, _lib.G9_SCHED_SK_HALF)
+
+
 def _workspace(lib, dt: int, M: int, N: int, K: int, sched: int, waves: int, dev, stream) -> tuple[int, int]:
-    if sched == _lib.G9_SCHED_SK:
+    if sched in _STREAMK:
         WORKSPACES.poll(dev, stream)
     need = lib.g9_workspace_size(dt, M, N, K, sched, waves)
     return WORKSPACES.get(dev, need, stream)
 
 
 def _after_launch(sched: int, dev, stream: int) -> None:
-    if CHECK_STREAMK and sched == _lib.G9_SCHED_SK:
+    if CHECK_STREAMK and sched in _STREAMK:
         WORKSPACES.check(dev, stream)
 
 

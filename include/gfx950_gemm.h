@@ -54,8 +54,11 @@ enum { G9_F16 = 0, G9_BF16 = 1, G9_BF8 = 2, G9_FP4 = 3, G9_FP4P = 4, G9_FP4K = 5
 
 /* Tile schedules.  G9_SCHED_SPLITK has no counterpart in the reference: it is
  * for callers whose grids leave most CUs idle (few-row GEMMs, one GPU's
- * shard of a sharded GEMM). */
-enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1, G9_SCHED_SPLITK = 2 };
+ * shard of a sharded GEMM).  G9_SCHED_SK_HALF is stream-K over 256 x 128
+ * tiles (a16w16 only, 4 waves; G9_ERR_SCHEDULE otherwise), bit-identical to
+ * data-parallel like G9_SCHED_SK, for grids with fewer 256 x 256 tiles than
+ * CUs; no counterpart in the reference either. */
+enum { G9_SCHED_DP = 0, G9_SCHED_SK = 1, G9_SCHED_SPLITK = 2, G9_SCHED_SK_HALF = 3 };
 
 /*
  * a16w16: FP16 or BF16 (`dtype` = G9_F16 / G9_BF16) in and out, fp32 accumulate.
@@ -79,9 +82,10 @@ int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, 
  * the reference.  Same arguments, kernels and results as g9_gemm_a16w16
  * without the workspace: the stream-K and split-K partials live in a static
  * device array of the library (one per GPU, held until the process ends) of
- * G9_NOALLOC_MAX_TILES fp32 partial tiles of 256 x 256 (64 MiB) plus a header
- * and flag words.  A call that needs more (stream-K on more tiles, split-K
- * with more segment tiles) returns G9_ERR_SCRATCH; data-parallel needs none.
+ * G9_NOALLOC_MAX_TILES fp32 partial tiles of 256 x 256, or twice as many of
+ * 256 x 128 (64 MiB), plus a header and flag words.  A call that needs more
+ * (stream-K on more tiles, split-K with more segment tiles) returns
+ * G9_ERR_SCRATCH; data-parallel needs none.
  * The call allocates nothing: a stream-K call first clears the array's flag
  * and error words with a fill kernel on `stream` (no memset), split-K writes
  * every partial it reads.  Calls share their GPU's array, so calls that may

@@ -294,7 +294,8 @@ def test_torch_matmul_f32_against_brute_force():
 # eventually has one free CU; the simulation checks it for the BASELINE
 # stream-K shapes and others under many residency limits.
 
-@pytest.mark.parametrize("tiles,stages", [(225, 256), (160, 128), (16, 256), (32, 128), (272, 128), (400, 128)])
+@pytest.mark.parametrize("tiles,stages", [(225, 256), (160, 128), (16, 256), (32, 128), (272, 128), (400, 128),
+                                          (450, 256), (320, 128)])
 def test_streamk_progress_under_partial_residency(tiles, stages):
     rng = np.random.default_rng(tiles * 1000 + stages)
     limits = [[1] * 8, [2] * 8, [32] * 8, [1, 32] * 4, [32, 1] * 4] + [list(rng.integers(1, 33, 8)) for _ in range(4)]

@@ -97,6 +97,23 @@ def test_noalloc_bf16_streamk_twice(gpu):
         assert torch.equal(got, want), (M, N, K)
 
 
+def test_noalloc_streamk_half_tiles_twice(gpu):
+    # 256x128 stream-K tiles (4 waves only): 450 tiles, then 60, in the same
+    # scratch array.
+    g = torch.Generator().manual_seed(83)
+    dt, code, sched = torch.float16, _lib.G9_F16, _lib.G9_SCHED_SK_HALF
+    for M, N, K in [(3840, 3840, 2048), (1920, 1024, 1024)]:
+        _say(f"noalloc stream-K 256x128 {M}x{N}x{K}")
+        a, b = _operands(g, M, N, K, dt, gpu)
+        want = _with_workspace(a, b, code, sched, 4)
+        got = torch.full((M, N), float("nan"), dtype=dt, device=gpu)
+        assert _call("noalloc", a, b, got, code, sched, 4) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (M, N, K)
+    c = torch.empty(64, 64, dtype=dt, device=gpu)
+    assert _call("noalloc", a[:64], b[:64], c, code, sched, 8) == _lib.G9_ERR_SCHEDULE
+
+
 def test_noalloc_rejects_more_than_the_scratch_holds(gpu):
     g = torch.Generator().manual_seed(80)
     M, N, K = 5120, 3328, 512  # 20 x 13 = 260 tiles > 256 partials
