@@ -53,6 +53,13 @@ HEADLINE_K = {"bf8": (16384, 3476.0, 3131.1), "mxfp4": (32768, 5804.0, 5195.9), 
 # kernels/gemm/intra_wave/a4w4/bench.py:137-146), mxfp4ps preshuffled.  Only
 # the 4-wave kernels read the last two as they are.
 FOUR_WAVE_ONLY = ("mxfp4ps", "mxfp4km")
+# How each MXFP4 case passes its E8M0 scales (recorded in its per_dtype entry).
+SCALE_LAYOUTS = {
+    "mxfp4": "row-major (M, K/32), contiguous",
+    "mxfp4km": "K-major: (K/32, M) storage viewed as (M, K/32), as the reference bench builds them "
+               "(kernels/gemm/intra_wave/a4w4/bench.py:137-146)",
+    "mxfp4ps": "preshuffled (quant.preshuffle_e8m0)",
+}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 # Flash-attention forward: the reference's tuned shape and its published
 # numbers (bf16, kernels/attention/README.md:619-632; no fp16 figure).
@@ -784,6 +791,8 @@ def main():
         key = dt + ("" if kk == K else f"_k{kk}") + ("" if w == 4 else "_8w")
         results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
                         "reference_tflops": ref, "K": kk, "rotating_sets": nsets, "waves": w}
+        if dt in SCALE_LAYOUTS:
+            results[key]["scales"] = SCALE_LAYOUTS[dt]
         msg = f"# {key}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak"
         if args.serialized:
             ms_s = time_serialized(launch)
