@@ -627,7 +627,6 @@ const char* g9_moe_kernel_name(int dtype, int out_dtype) {
 }
 
 size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedule, int waves) {
-  (void)waves;
   if (M <= 0 || N <= 0 || K <= 0 || stage_k(dtype) == 0) return 0;
   const long long tiles = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
   if (schedule == G9_SCHED_SPLITK) {
@@ -635,7 +634,11 @@ size_t g9_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int schedul
     const int S = cus > 0 ? g9_splitk_factor(tiles, (int)((K + stage_k(dtype) - 1) / stage_k(dtype)), cus) : 1;
     return S > 1 ? splitk_bytes(tiles * S) : 0;
   }
-  if (schedule == G9_SCHED_SK_HALF) return streamk_half_bytes(((M + kTile - 1) / kTile) * ((N + 127) / 128));
+  if (schedule == G9_SCHED_SK_HALF) {
+    // Only FP16/BF16 with 4 waves run this schedule (the launch rejects the rest).
+    if ((dtype != G9_F16 && dtype != G9_BF16) || waves != 4) return 0;
+    return streamk_half_bytes(((M + kTile - 1) / kTile) * ((N + 127) / 128));
+  }
   if (schedule != G9_SCHED_SK) return 0;
   return streamk_bytes(tiles);
 }

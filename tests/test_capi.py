@@ -129,11 +129,11 @@ def test_splitk_factor_invariants():
 
 def _flags_base(ws_bytes):
     """Start of the partials in a workspace of ws_bytes: behind the header and
-    the flag words g9_workspace_init clears for that size (one per tile whose
-    partial fits, plus one, rounded up to 256 bytes)."""
-    tile = 256 * 256 * 4
-    max_tiles = (ws_bytes - 256) // tile + 1
-    return 256 + -(-max_tiles * 4 // 256) * 256
+    the flag words g9_workspace_init clears for that size (one per 256x128
+    partial that fits, plus one, rounded up to 256 bytes)."""
+    unit = 256 * 128 * 4
+    max_units = (ws_bytes - 256) // unit + 1
+    return 256 + -(-max_units * 4 // 256) * 256
 
 
 def test_workspace_size():
@@ -149,6 +149,15 @@ def test_workspace_size():
         ws = lib.g9_workspace_size(_lib.G9_F16, M, N, 1024, _lib.G9_SCHED_SK, 4)
         assert _flags_base(ws) + tiles * 256 * 256 * 4 <= ws, (M, N)
         assert _flags_base(ws) >= 256 + 4 * (tiles + 1)
+        # 256x128 tiles: twice as many flags, each partial half the size.
+        tiles_h = -(-M // 256) * -(-N // 128)
+        wh = lib.g9_workspace_size(_lib.G9_F16, M, N, 1024, _lib.G9_SCHED_SK_HALF, 4)
+        assert _flags_base(wh) + tiles_h * 256 * 128 * 4 <= wh, (M, N)
+        assert _flags_base(wh) >= 256 + 4 * (tiles_h + 1)
+    # Only FP16/BF16 with 4 waves run 256x128 tiles.
+    assert lib.g9_workspace_size(_lib.G9_BF16, 3840, 3840, 1024, _lib.G9_SCHED_SK_HALF, 4) > 0
+    assert lib.g9_workspace_size(_lib.G9_F16, 3840, 3840, 1024, _lib.G9_SCHED_SK_HALF, 8) == 0
+    assert lib.g9_workspace_size(_lib.G9_BF8, 3840, 3840, 1024, _lib.G9_SCHED_SK_HALF, 4) == 0
 
 
 def test_streamk_rejects_a_workspace_256_bytes_short():
@@ -159,6 +168,17 @@ def test_streamk_rejects_a_workspace_256_bytes_short():
     short = lib.g9_gemm_a16w16(FAKE, FAKE, FAKE, M, N, K, K, 1, 1, K, N, 1, _lib.G9_F16, _lib.G9_SCHED_SK, 4,
                                FAKE, ws - 256, None)
     assert short == _lib.G9_ERR_WORKSPACE
+
+
+def test_streamk_half_validation():
+    """Validation only: rejected before any launch (no GPU work)."""
+    lib = _lib.load()
+    M, N, K = 3840, 3840, 1024
+    ws = lib.g9_workspace_size(_lib.G9_F16, M, N, K, _lib.G9_SCHED_SK_HALF, 4)
+    args = (FAKE, FAKE, FAKE, M, N, K, K, 1, 1, K, N, 1, _lib.G9_F16, _lib.G9_SCHED_SK_HALF)
+    assert lib.g9_gemm_a16w16(*args, 8, FAKE, ws, None) == _lib.G9_ERR_SCHEDULE
+    assert lib.g9_gemm_a16w16(*args, 4, FAKE, ws - 256, None) == _lib.G9_ERR_WORKSPACE
+    assert lib.g9_gemm_a16w16_noalloc(*args, 8, None) == _lib.G9_ERR_SCHEDULE
 
 
 def test_b_operand_rows_not_16_byte_aligned_are_repacked():
