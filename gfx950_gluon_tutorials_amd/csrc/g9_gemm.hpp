@@ -296,9 +296,11 @@ constexpr bool kChunkScales = OP == Op::FP4P || kTrScales<OP, G>;
 // 16h + 0, 2, 4 (the remaining parts of the chunk one ahead), each at least
 // 10 regions before the chunk is first read (position 16h + 14 reads the next
 // chunk's first stage) and after the slot's previous chunk was last read
-// (position 16h + 13).  A region waits for the DMAs issued 7 regions earlier:
-// vmcnt(number of DMAs issued in the 6 regions between), a constant per body
-// position because the pattern repeats every 16 regions.
+// (position 16h + 13); all of these positions are even, so each has a
+// barrier under either barrier pattern.  With a barrier per region, a region
+// waits for the DMAs issued 7 regions earlier: vmcnt(number of DMAs issued in
+// the 6 regions between), a constant per body position because the pattern
+// repeats every 16 regions (vm_wait_hb: the half-barrier pattern).
 template <Op OP, class G>
 struct Shape {
   static constexpr int KS = G::NC / OpInfo<OP>::kChunksPerMfma;  // MFMA steps per stage
@@ -328,6 +330,14 @@ struct Shape {
   static constexpr int vm_wait_pp(int pos) {
     int n = 0;
     for (int q = 0; q <= 5; ++q) n += dmas(((pos - q) % kRegions + kRegions) % kRegions);
+    return n;
+  }
+  // Barriers at even positions only (kHalfBarrier): an even region's barrier
+  // also publishes the data the next (odd) region reads, so it waits for the
+  // DMAs issued 5 regions earlier: vmcnt(DMAs of the 4 regions between).
+  static constexpr int vm_wait_hb(int pos) {
+    int n = 0;
+    for (int q = 1; q <= 4; ++q) n += dmas(((pos - q) % kRegions + kRegions) % kRegions);
     return n;
   }
   static_assert(vm_wait(0) < 64 && vm_wait_pp(0) < 64, "vmcnt is 6 bits");
@@ -1099,6 +1109,24 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
   __builtin_amdgcn_sched_barrier(0);
 }
 
+#ifndef G9_PINGPONG
+#define G9_PINGPONG 1
+#endif
+// 8-wave kernels run the ping-pong schedule below.
+template <class G>
+constexpr bool kPingPong = G9_PINGPONG != 0 && G::NW == 8;
+#ifndef G9_HALF_BARRIER
+#define G9_HALF_BARRIER 1
+#endif
+// The other FP16, BF16 and MXFP4 kernels pass a barrier at even body
+// positions only (see stage()): measured interleaved on two boxes against a
+// barrier in every region, 0.8-1.0% less time for FP16, 0.4-1.3% for BF16,
+// 0.5-1.2% for MXFP4 (all three scale layouts), results identical.  BF8's
+// regions are twice as long (32-cycle MFMAs) and it measured no faster, so it
+// keeps a barrier per region.
+template <Op OP, class G>
+constexpr bool kHalfBarrier = G9_HALF_BARRIER != 0 && !kPingPong<G> && OP != Op::BF8;
+
 // The quadrant region at body position POS (region POS % 4 of stage s + POS / 4,
 // with s the body's first stage): MFMAs of (bx, ay) into acc, LDS reads of
 // sub-buffer RX/RSLOT into nxt, DMA of stage `ds` into sub-buffer DX/DSLOT.
@@ -1110,14 +1138,19 @@ G9_DEV void region_slot(const Pipe<OP, G>& P, rsrc_t r, u32 soff, u32 soff_sc, u
 //                                             wave done reading the sub-buffer
 //                                             refilled now
 //   remaining MFMAs with the reads and DMAs interleaved
+// kHalfBarrier: odd positions wait for the previous region's reads only and
+// pass no barrier (their MFMAs, reads and DMAs in the same slots); even
+// positions wait for the DMAs of 5 regions earlier (vm_wait_hb).
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS>
 G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP, G>& sr, const FragSet<G>& bx,
                    const FragSet<G>& ay, FragSet<G>& nxt) {
   constexpr int NF = RX < 2 ? G::FM : G::FN;
   using S = Slots<OP, G, NF>;
   using Sh = Shape<OP, G>;
+  constexpr bool kBar = !kHalfBarrier<OP, G> || POS % 2 == 0;
+  constexpr int kVm = !kHalfBarrier<OP, G> ? Sh::vm_wait(POS) : kBar ? Sh::vm_wait_hb(POS) : 63;
   __builtin_amdgcn_sched_barrier(0);
-  waitcnt<Sh::vm_wait(POS), 0>();
+  waitcnt<kVm, 0>();
   const rsrc_t r = P.src(DX);
   const u32 soff = P.stage_off(ds);
   const u32 mb = opaque_s(P.mrow);
@@ -1129,7 +1162,7 @@ G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP,
   [&]<int... K>(std::integer_sequence<int, K...>) {
     (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K>(P, r, soff, soff_sc, mb, ms, acc, sr, bx, ay, nxt), ...);
   }(std::make_integer_sequence<int, S::kPre>{});
-  barrier();
+  if constexpr (kBar) barrier();
   [&]<int... K>(std::integer_sequence<int, K...>) {
     (region_slot<OP, G, RX, RSLOT, DX, DSLOT, POS, K + S::kPre>(P, r, soff, soff_sc, mb, ms, acc, sr, bx, ay, nxt),
      ...);
@@ -1159,12 +1192,6 @@ G9_DEV void region(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP,
 //    after that barrier.  The lagging group waits one region earlier than its
 //    own reads need, so the DMA lead is 6 regions instead of 7.
 // ---------------------------------------------------------------------------
-#ifndef G9_PINGPONG
-#define G9_PINGPONG 1
-#endif
-template <class G>
-constexpr bool kPingPong = G9_PINGPONG != 0 && G::NW == 8;
-
 template <Op OP, class G, int RX, int RSLOT, int DX, int DSLOT, int POS>
 G9_DEV void region_pp(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<OP, G>& sr, const FragSet<G>& bx,
                       const FragSet<G>& ay, FragSet<G>& nxt) {
@@ -1208,6 +1235,17 @@ G9_DEV void region_pp(const Pipe<OP, G>& P, int s, int ds, QAcc<G>& acc, ScRegs<
 // fragments in x; B1 fragments go to y, and after they are consumed the next
 // stage's B0 fragments go to y as well.  Odd stages (slot 1): B0 in y; B1 to
 // x, then the next stage's B0.
+//
+// Each region reads one sub-buffer (B1, A1, then the next stage's A0 and B0)
+// and refills one that every wave has finished reading, i.e. one read before
+// the last barrier.  With a barrier in every region that is the sub-buffer
+// read in the previous region (the last region refills the next stage's A0
+// with stage + 3).  kHalfBarrier: an odd region's last barrier is its
+// predecessor's, so every region refills the sub-buffer read two regions
+// earlier: stage K's four regions refill A0, B0, B1, A1 of its slot with stage
+// K + 2, the prologue's order.  Each sub-buffer is read again 6 regions after
+// its refill, at an even position or right after one; the even region's wait
+// (vm_wait_hb) covers both.
 template <Op OP, class G, int K>
 G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, ScRegs<OP, G>& sr, FragSet<G>& at, FragSet<G>& ab,
                   FragSet<G>& x, FragSet<G>& y) {
@@ -1219,7 +1257,15 @@ G9_DEV void stage(const Pipe<OP, G>& P, int s, Acc<G>& acc, ScRegs<OP, G>& sr, F
     else
       region<OP, G, RX, RSLOT, DX, DSLOT, P_>(P, s, ds, a, sr, bx, ay, nxt);
   };
-  if constexpr (K % 2 == 0) {
+  if constexpr (kHalfBarrier<OP, G>) {
+    constexpr int sl = K % 2, nx = 1 - sl;
+    FragSet<G>& b0 = sl ? y : x;  // this stage's B0 fragments
+    FragSet<G>& b1 = sl ? x : y;  // its B1, then the next stage's B0
+    rg.template operator()<3, sl, 0, sl, POS + 0>(s + K + 2, acc[0][0], b0, at, b1);
+    rg.template operator()<1, sl, 2, sl, POS + 1>(s + K + 2, acc[0][1], b1, at, ab);
+    rg.template operator()<0, nx, 3, sl, POS + 2>(s + K + 2, acc[1][1], b1, ab, at);
+    rg.template operator()<2, nx, 1, sl, POS + 3>(s + K + 2, acc[1][0], b0, ab, b1);
+  } else if constexpr (K % 2 == 0) {
     rg.template operator()<3, 0, 2, 0, POS + 0>(s + K + 2, acc[0][0], x, at, y);
     rg.template operator()<1, 0, 3, 0, POS + 1>(s + K + 2, acc[0][1], y, at, ab);
     rg.template operator()<0, 1, 1, 0, POS + 2>(s + K + 2, acc[1][1], y, ab, at);
@@ -1299,7 +1345,9 @@ G9_DEV void mainloop(const GemmParams& p, char* smem, int tm, int tn, int s0, in
     P.template gather_scales<2>(x);
   }
   barrier();
-  P.template issue<0, 0>(s0 + 2);
+  // The refill of A0's slot 0 the region before the loop would issue (with a
+  // barrier per region; kHalfBarrier: the loop's first region issues it).
+  if constexpr (!kHalfBarrier<OP, G>) P.template issue<0, 0>(s0 + 2);
   // Ping-pong: waves 4-7 start one cluster behind.
   const bool lag = kPingPong<G> && P.wave >= 4;
   if (lag) barrier();
