@@ -758,21 +758,24 @@ struct Pipe {
       } else if constexpr (kTrScales<OP, G>) {
         // KM layout of a chunk slot: half tile X at X * 4096, its part jj
         // (rows 32 jj .. 32 jj + 31) at + jj * 1024; in a part, group G
-        // (0..31) is a 32-byte row at position p(G) = (G >> 2) + 8 (G & 3),
-        // holding the part's four 8-row octets, octet o at 8 (o ^ 2 (G & 1)):
-        // the scales of rows 8o .. 8o + 7, in row order.
+        // (0..31) is a 32-byte row at position p(G) = ((G >> 2) ^ (G & 2)) +
+        // 8 (G & 3), holding the part's four 8-row octets, octet o at
+        // 8 (o ^ 2 (G & 1)): the scales of rows 8o .. 8o + 7, in row order.
         // ds_read_b64_tr_b8 gives lane 8a + b of each 16-lane group byte b of
         // the 8-byte units addressed by lanes a, a + 2, ..., a + 14 of the
         // group (measured on gfx950).  Lane 16g + 2k + a addresses the unit
         // of group 4k + g and octet a of the fragment's two, so lane (g, row
         // rr) receives the scales of its row for groups g, 4 + g, ..., 28 + g:
         // byte 2 st + h is stage st, MFMA step h, as the MFMAs take them.
-        // Per 32 lanes (two lane groups) the 16 units sit on 64 distinct
-        // banks.
+        // Per 32 lanes (two lane groups, one value of g & 2) the 16 units sit
+        // on 64 distinct banks.  The XOR of G & 2 in p(G) is for the
+        // transpose's writes below: without it the two lanes of a write pass
+        // whose groups differ only in bit 1 hit the same banks (measured,
+        // 1152 conflict cycles per workgroup).
         const int g = lane >> 4, k = (lane >> 1) & 7, a = lane & 1;
 #pragma unroll
         for (int f2 = 0; f2 < 2; ++f2) {
-          const u32 off = 32u * (u32)(k + 8 * g) + 8u * (u32)((2 * f2 + a) ^ (2 * (g & 1)));
+          const u32 off = 32u * (u32)((k ^ (g & 2)) + 8 * g) + 8u * (u32)((2 * f2 + a) ^ (2 * (g & 1)));
           bS[0][f2] = opaque(lds0 + kScaleBase + (u32)wm * 2048u + off);
           bS[1][f2] = opaque(lds0 + kScaleBase + 8192u + (u32)wn * 2048u + off);
         }
@@ -789,8 +792,10 @@ struct Pipe {
           for (int i = 0; i < 2; ++i)
             tb[i] = opaque(msc + 512u * (u32)a + 256u * (u32)i + 32u * (u32)k + 16u * (u32)(((g >> 1) ^ a) ^ i) +
                            8u * (u32)(g & 1));
+          // Lane 16g + 8a + b writes group G = 8 (g ^ 2a) + b at p(G); a write
+          // pass of 8 lanes (one g and a) covers 32 distinct banks.
           const int a2 = (lane >> 3) & 1, b = lane & 7;
-          const int pg = 2 * (g ^ (2 * a2)) + (b >> 2) + 8 * (b & 3);
+          const int pg = ((2 * (g ^ (2 * a2)) + (b >> 2)) ^ (b & 2)) + 8 * (b & 3);
           tw = opaque(msc + 32u * (u32)pg + 16u * (u32)(a2 ^ (b & 1)));
         }
         sel = 0;

@@ -73,20 +73,26 @@ def xform_read_addr(i, lane):
     return 512 * a + 256 * i + 32 * k + 16 * (((g >> 1) ^ a) ^ i) + 8 * (g & 1)
 
 
+def xform_write_addr(lane):
+    """tw: lane 16g + 8a + b writes its two units (group G = 8 (g ^ 2a) + b)
+    at 32 p + 16 (a ^ (b & 1)), p = ((2 (g ^ 2a) + (b >> 2)) ^ (b & 2)) +
+    8 (b & 3)."""
+    g, a2, b = lane >> 4, (lane >> 3) & 1, lane & 7
+    pg = ((2 * (g ^ (2 * a2)) + (b >> 2)) ^ (b & 2)) + 8 * (b & 3)
+    return 32 * pg + 16 * (a2 ^ (b & 1))
+
+
 def xform(lds, xw):
     """The in-place transpose of wave xw's four parts: two transpose reads
     per part (tb[i]: lane 16g + 2k + a at 512a + 256i + 32k + 16((g >> 1) ^
-    a ^ i) + 8(g & 1)), then one 16-byte write per lane 16g + 8a + b (tw: at
-    32 p + 16 (a ^ (b & 1)), p = 2 (g ^ 2a) + (b >> 2) + 8 (b & 3)) of its
-    two units, read 0's first."""
+    a ^ i) + 8(g & 1)), then one 16-byte write per lane (xform_write_addr)
+    of its two units, read 0's first."""
     msc = xw * HALF
     for j in range(4):
         got = [tr_read(lds, [msc + 1024 * j + xform_read_addr(i, lane) for lane in range(64)]) for i in range(2)]
         writes = []
         for lane in range(64):
-            g, a2, b = lane >> 4, (lane >> 3) & 1, lane & 7
-            pg = 2 * (g ^ (2 * a2)) + (b >> 2) + 8 * (b & 3)
-            writes.append((msc + 1024 * j + 32 * pg + 16 * (a2 ^ (b & 1)), got[0][lane] + got[1][lane]))
+            writes.append((msc + 1024 * j + xform_write_addr(lane), got[0][lane] + got[1][lane]))
         # The writes of a part cover exactly its KiB, once each.
         covered = sorted(w for w, _ in writes)
         assert covered == list(range(msc + 1024 * j, msc + 1024 * (j + 1), 16))
@@ -97,11 +103,12 @@ def xform(lds, xw):
 def mfma_read(lds, side, wave_col, F):
     """The chunk-scale read of fragment F of sub-buffer X = side (0..3) by a
     wave in row/column wave_col: bS[X >= 2][F & 1] + (X & 1) 4096 + (F / 2)
-    1024, with lane 16g + 2k + a at 32 (k + 8g) + 8 ((2 (F & 1) + a) ^ 2 (g & 1))."""
+    1024, with lane 16g + 2k + a at 32 ((k ^ (g & 2)) + 8g) + 8 ((2 (F & 1) + a)
+    ^ 2 (g & 1))."""
     addrs = []
     for lane in range(64):
         g, k, a = lane >> 4, (lane >> 1) & 7, lane & 1
-        off = 32 * (k + 8 * g) + 8 * ((2 * (F & 1) + a) ^ (2 * (g & 1)))
+        off = 32 * ((k ^ (g & 2)) + 8 * g) + 8 * ((2 * (F & 1) + a) ^ (2 * (g & 1)))
         base = (8192 if side >= 2 else 0) + 2048 * wave_col + off
         addrs.append(base + (side & 1) * 4096 + (F // 2) * 1024)
     return tr_read(lds, addrs), addrs
@@ -248,3 +255,17 @@ def test_transpose_reads_are_bank_conflict_free_per_32_lanes():
         for h in range(2):
             assert len(set(_banks(addrs[32 * h:32 * h + 32]))) == 64
 
+
+def test_transpose_writes_are_bank_conflict_free_per_8_lanes():
+    # A 16-byte write is served 8 lanes at a time (the previous group-row
+    # order, p = (G >> 2) + 8 (G & 3), measured 1152 conflict cycles per
+    # workgroup, which this pass model gives as 8 per write): the 32 banks of
+    # each pass of 8 lanes must be distinct.
+    addrs = [xform_write_addr(lane) for lane in range(64)]
+    for p0 in range(0, 64, 8):
+        assert len(set(_banks(addrs[p0:p0 + 8], width=16))) == 32, p0
+    old = []
+    for lane in range(64):
+        g, a2, b = lane >> 4, (lane >> 3) & 1, lane & 7
+        old.append(32 * (2 * (g ^ (2 * a2)) + (b >> 2) + 8 * (b & 3)) + 16 * (a2 ^ (b & 1)))
+    assert any(len(set(_banks(old[p0:p0 + 8], width=16))) < 32 for p0 in range(0, 64, 8))
