@@ -136,6 +136,33 @@ def test_a16w16_cpu_plumbing_config(gpu, schedule):
     _check_f16(c, R.a16w16_ref(a.numpy(), b.numpy()), K=1024, sigma=1.0)
 
 
+@pytest.mark.parametrize("M,N", [(1, 1), (129, 127), (130, 129), (255, 136), (256, 257), (300, 390)])
+@pytest.mark.parametrize("pad", [0, 3, 8])
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_a16w16_epilogue_edges_exact(gpu, M, N, pad, waves, schedule):
+    # Small-integer operands make every output exact in fp32 and fp16, so the
+    # kernel must match the oracle bit for bit.  M and N fall on both sides of
+    # the 128-row / 128-column quadrant boundaries of a 256x256 tile (the
+    # 4-wave epilogue stores quadrant by quadrant), and C is a view of a wider
+    # NaN-filled buffer (row stride N + pad; pad 3 misaligns the 16-byte
+    # stores): nothing outside the view may change.
+    K = 64
+    _say(f"a16w16 epilogue edges {M}x{N}x{K} pad {pad} {waves}w {schedule}")
+    rng = np.random.default_rng(M * 1000 + N + pad)
+    a = rng.integers(-3, 4, (M, K)).astype(np.float16)
+    b = rng.integers(-3, 4, (N, K)).astype(np.float16)
+    full = torch.full((M, N + pad), float("nan"), dtype=torch.float16, device=gpu)
+    c = full[:, :N]
+    _launch.gemm_a16w16(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu).T, c, schedule=schedule,
+                        waves=waves)
+    torch.cuda.synchronize()
+    _check_streamk_clean(gpu)
+    np.testing.assert_array_equal(_f32(c), R.a16w16_ref(a, b))
+    if pad:
+        assert torch.isnan(full[:, N:]).all()
+
+
 @pytest.mark.parametrize("M,N,K", [(300, 200, 512), (257, 129, 64), (64, 1000, 192), (1, 8, 128), (513, 77, 320)])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_a16w16_ragged_shapes(gpu, M, N, K, dtype):
