@@ -18,14 +18,17 @@
 // Per stage every wave runs four "quadrant regions" in the order
 // Q00 (A0 x B0), Q01 (A0 x B1), Q11 (A1 x B1), Q10 (A1 x B0).  Each region
 // issues its MFMAs on operand fragments already in registers, reads the next
-// region's operand set from LDS into registers, and refills, by LDS-DMA, the
-// sub-buffer whose last reads finished in the previous region.  A region
-// starts with `s_waitcnt vmcnt(N) lgkmcnt(0)` (N: the DMAs issued since the
-// ones it needs), issues its first MFMAs, then `s_barrier`: the sub-buffer read
-// during a region was requested seven regions earlier, so the DMA latency
-// budget is 1.5 stages and one barrier per region suffices.  The B operand
+// region's operand set from LDS into registers, and refills, by LDS-DMA, a
+// sub-buffer every wave has finished reading.  A region starts with
+// `s_waitcnt vmcnt(N) lgkmcnt(0)` (N: the DMAs issued since the ones it
+// needs), issues its first MFMAs, then `s_barrier`.  With a barrier in every
+// region (BF8) a region refills the sub-buffer read in the previous one,
+// requested seven regions before it is read again (a DMA latency budget of 1.5
+// stages); the other 4-wave kernels pass a barrier in even regions only, and
+// refill the sub-buffer read two regions earlier (stage()).  The B operand
 // registers alternate roles between even and odd stages, so the loop body
-// covers two stages (eight for FP4: two scale chunks).
+// covers two stages (eight for FP4: two scale chunks).  The 8-wave kernels run
+// the same regions in a ping-pong (region_pp).
 //
 // LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk slot
 // c ^ ((r >> 1) & 7).  A ds_read_b128 by 16 consecutive lanes (16 rows, one
@@ -36,7 +39,8 @@
 // MFMA operands are swapped (the B fragment is the MFMA's A operand), so lane l
 // ends with C[m0 + l%16][n0 + 4*(l/16) + 0..3]: four consecutive output
 // columns, which the epilogue writes to LDS as one 8-byte store and then streams
-// out as coalesced 16-byte row chunks.
+// out as coalesced 16-byte row chunks (4-wave: quadrant by quadrant, each
+// quadrant's stores beside the next one's conversion).
 //
 // Three tile schedules drive this pipeline: gemm_dp (one tile per workgroup),
 // gemm_sk (persistent workgroups over (tile, stage) ranges with a K-ordered
