@@ -21,7 +21,8 @@ whatever the waves' relative timing between barriers:
   covers it, and its writes reach a barrier before any wave reads the chunk.
 
 Plausible mistakes (refilling the sub-buffer read in the previous region under
-half barriers, waiting for one region's DMAs too few) fail the checks.
+half barriers, waiting for one region's DMAs too few) fail the checks.  The
+8-wave ping-pong (region_pp) is replayed the same way, phase by phase.
 """
 
 import pytest
@@ -238,3 +239,126 @@ def test_a_late_transpose_write_is_caught(half):
     # region that first reads the chunk, after that region's barrier.
     errors = run(12, scaled=True, half=half, xform=True, write_shift=1)
     assert any("before its transpose reached a barrier" in e for e in errors)
+
+
+# ---------------------------------------------------------------------------
+# 8-wave ping-pong (region_pp): waves 0-3 (group 0) and 4-7 (group 1) run the
+# same clusters one barrier apart, so between two barriers exactly one group
+# runs a memory cluster (its LDS reads, its half of every DMA, then lgkmcnt(0)
+# and vmcnt(vm_wait_pp)) while the other runs MFMAs.  Phase p >= 1 holds
+# group 0's memory cluster of region (p - 1) / 2 (p odd) or group 1's of
+# region (p - 2) / 2 (p even); phase 0 holds both groups' prologue refill.
+# A sub-buffer's contents are complete only once both groups' DMAs of it have
+# landed, each followed by a barrier; a refill by either group must come in a
+# later phase than every read of the previous contents.
+# ---------------------------------------------------------------------------
+D8 = 2   # operand DMAs per sub-buffer per wave (8 waves)
+SP8 = 2  # scale-chunk parts per wave (8 waves)
+
+
+def sc_part8(pos, scaled):
+    if not scaled:
+        return -1
+    q = pos % 16
+    if q == 14:
+        return 0
+    if q % 2 == 0 and q // 2 + 1 < SP8:
+        return q // 2 + 1
+    return -1
+
+
+def vm_wait_pp(pos, scaled, back=5):
+    R = body_regions(scaled)
+    return sum(D8 + (1 if sc_part8((pos - q) % R, scaled) >= 0 else 0) for q in range(0, back + 1))
+
+
+def run_pingpong(nst, scaled, back=5):
+    """Replays the 8-wave mainloop() for stages [0, nst); returns the violations."""
+    R = body_regions(scaled)
+    errors = []
+    issued = [[], []]          # per group: list of DMA keys (one entry per instruction)
+    frontier = [[], []]        # per group: (phase after which, DMAs complete)
+    content = {}               # key -> (content, {group: last instruction index})
+    reads = {}                 # key -> phases of reads of the current contents
+
+    def dma(g, phase, key, c, n):
+        if any(p >= phase for p in reads.get(key, [])):
+            errors.append(f"group {g} refills {key} with {c} in phase {phase} before a read of it ended")
+        issued[g].extend([key] * n)
+        old = content.get(key)
+        idx = dict(old[1]) if old and old[0] == c else {}
+        idx[g] = len(issued[g]) - 1
+        content[key] = (c, idx)
+        if not old or old[0] != c:
+            reads[key] = []
+
+    def wait(g, phase, count):
+        frontier[g].append((phase, len(issued[g]) - count))
+
+    def read(g, phase, key, c):
+        got = content.get(key)
+        if got is None or got[0] != c or set(got[1]) != {0, 1}:
+            errors.append(f"group {g} reads {key} in phase {phase} wanting {c}, holds {got and got[0]}")
+            return
+        for h, idx in got[1].items():
+            if not any(f > idx and p < phase for p, f in frontier[h]):
+                errors.append(f"group {g} reads {key} ({c}) in phase {phase} before group {h}'s DMA landed")
+        reads[key].append(phase)
+
+    def both_dma(phase, key, c, n):
+        for g in (0, 1):
+            dma(g, phase, key, c, n)
+
+    # Prologue (both groups in lockstep, phases -3 .. 0).
+    if scaled:
+        for part in range(SP8):
+            both_dma(-3, ("C", 0, part), 0, 1)
+    for s in (0, 1):
+        for x in (A0, B0, B1, A1):
+            both_dma(-3, ("S", x, s % 2), s, D8)
+    if scaled:
+        both_dma(-3, ("C", 1, 0), 1, 1)
+    first = 5 * D8 + (1 if scaled else 0)
+    for g in (0, 1):
+        wait(g, -3, first)                       # then a barrier
+    for g in (0, 1):
+        read(g, -2, ("S", A0, 0), 0)
+        read(g, -2, ("S", B0, 0), 0)
+        if scaled:
+            for part in range(SP8):
+                read(g, -2, ("C", 0, part), 0)
+        wait(g, -2, first)                       # then a barrier
+    both_dma(0, ("S", A0, 0), 2, D8)             # before group 1's extra barrier
+    for r in range(4 * nst):
+        k, q, pos = r // 4, r % 4, r % R
+        rx, rs, dx, ds = stage_table(k, half=False)[q]
+        for g in (0, 1):
+            phase = 2 * r + 1 + g
+            if rs < nst:
+                read(g, phase, ("S", rx, rs % 2), rs)
+                if scaled:
+                    for part in range(SP8):
+                        read(g, phase, ("C", (rs // CHUNK) % 2, part), rs // CHUNK)
+            dma(g, phase, ("S", dx, ds % 2), ds, D8)
+            part = sc_part8(pos, scaled)
+            if part >= 0:
+                h = 2 * (r // R) + pos // 16
+                c = h + (2 if part == 0 else 1)
+                dma(g, phase, ("C", c % 2, part), c, 1)
+            wait(g, phase, vm_wait_pp(pos, scaled, back))
+    return errors
+
+
+@pytest.mark.parametrize("nst", list(range(1, 19)) + [24, 33])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_pingpong_schedule_is_race_free(nst, scaled):
+    assert run_pingpong(nst, scaled) == []
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+def test_pingpong_waiting_one_region_short_is_caught(scaled):
+    # Planted: a memory cluster leaving its DMAs of 7 regions outstanding
+    # instead of 6 lets the leading group read a sub-buffer the lagging
+    # group's DMAs have not filled yet.
+    errors = run_pingpong(12, scaled, back=6)
+    assert any("DMA landed" in e for e in errors)
