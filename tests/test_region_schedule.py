@@ -22,7 +22,8 @@ whatever the waves' relative timing between barriers:
 
 Plausible mistakes (refilling the sub-buffer read in the previous region under
 half barriers, waiting for one region's DMAs too few) fail the checks.  The
-8-wave ping-pong (region_pp) is replayed the same way, phase by phase.
+8-wave ping-pong (region_pp) is replayed the same way, phase by phase, and
+so is the 256x128 stream-K tile's three-slot schedule (mainloop_h).
 """
 
 import pytest
@@ -362,3 +363,48 @@ def test_pingpong_waiting_one_region_short_is_caught(scaled):
     # group's DMAs have not filled yet.
     errors = run_pingpong(12, scaled, back=6)
     assert any("DMA landed" in e for e in errors)
+
+
+# ---------------------------------------------------------------------------
+# 256x128 stream-K tiles (mainloop_h): sub-buffers A0, A1, B0 in three slots
+# (stage s in slot s % 3), two regions per stage with a barrier each.  Region
+# 0 of stage s reads A1(s) and B0(s + 1) and refills B0 and the first half of
+# A0's rows of slot s % 3 with stage s + 3; region 1 reads A0(s + 1) and
+# B0(s + 1) and refills the other half of A0 and A1.  Each region waits for
+# all but the DMAs of the three regions before it (kHnVmWait).
+# ---------------------------------------------------------------------------
+def run_hn(nst, back=3):
+    w = Wave()
+    for s in (0, 1, 2):
+        w.dma(("B0", s), s, D)
+        w.dma(("A0lo", s), s, 2)
+        w.dma(("A0hi", s), s, 2)
+        w.dma(("A1", s), s, D)
+    w.sync(7 * D, barrier=True)
+    for key in ("A0lo", "A0hi", "B0"):
+        w.read((key, 0), 0)
+    for r in range(2 * nst):
+        s, half = r // 2, r % 2
+        w.sync(back * 6, barrier=True)
+        if half == 0:
+            reads = [(("A1", s % 3), s), (("B0", (s + 1) % 3), s + 1)]
+            refills = [("B0", D), ("A0lo", 2)]
+        else:
+            reads = [(("A0lo", (s + 1) % 3), s + 1), (("A0hi", (s + 1) % 3), s + 1), (("B0", (s + 1) % 3), s + 1)]
+            refills = [("A0hi", 2), ("A1", D)]
+        for key, want in reads:
+            if want < nst:
+                w.read(key, want)
+        for x, n in refills:
+            w.dma((x, s % 3), s + 3, n)
+    return w.errors
+
+
+@pytest.mark.parametrize("nst", list(range(1, 20)) + [25, 36])
+def test_half_tile_streamk_schedule_is_race_free(nst):
+    assert run_hn(nst) == []
+
+
+def test_half_tile_waiting_one_region_short_is_caught():
+    errors = run_hn(12, back=4)
+    assert any("before its DMA landed" in e for e in errors)
