@@ -76,6 +76,7 @@ SIGNATURES = {
     "g9_workspace_error": (_int, [_vp, _sz, _vp, ctypes.POINTER(_int)]),
     "g9_workspace_watch": (_int, [_vp, _sz, _vp, _vp]),
     "g9_set_streamk_spin_limit": (ctypes.c_uint32, [ctypes.c_uint32]),
+    "g9_transpose_u8": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "g9_noalloc_error": (_int, [_vp, ctypes.POINTER(_int)]),
     "g9_kernel_name": (ctypes.c_char_p, [_int, _int, _int, _int]),
     "g9_status_string": (ctypes.c_char_p, [_int]),

@@ -676,6 +676,44 @@ __global__ void set_words2(u32* p, u32 lo, u32 hi) {
     p[1] = hi;
   }
 }
+// dst (cols x rows, row stride dst_ld) = transpose of src (rows x cols, row
+// stride src_ld), bytes, through a 64 x 64 LDS tile per workgroup.  Full
+// tiles with 4-byte aligned rows move dwords: 16 lanes read a source row's 64
+// bytes, and each lane then packs 4 source rows' bytes of one column into a
+// dword of the destination row; edge tiles and unaligned operands go byte by
+// byte.
+__global__ __launch_bounds__(256) void transpose_u8(const unsigned char* src, long long rows, long long cols,
+                                                    long long src_ld, unsigned char* dst, long long dst_ld,
+                                                    int words) {
+  __shared__ __attribute__((aligned(4))) unsigned char tile[64][68];
+  const long long r0 = (long long)blockIdx.y * 64, c0 = (long long)blockIdx.x * 64;
+  const bool full = words && r0 + 64 <= rows && c0 + 64 <= cols;
+  if (full) {
+    for (int i = threadIdx.x; i < 64 * 16; i += 256) {
+      const int r = i >> 4, w = i & 15;
+      *reinterpret_cast<u32*>(&tile[r][4 * w]) = *reinterpret_cast<const u32*>(src + (r0 + r) * src_ld + c0 + 4 * w);
+    }
+  } else {
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      const int r = i >> 6, c = i & 63;
+      if (r0 + r < rows && c0 + c < cols) tile[r][c] = src[(r0 + r) * src_ld + c0 + c];
+    }
+  }
+  __syncthreads();
+  if (full) {
+    for (int i = threadIdx.x; i < 64 * 16; i += 256) {
+      const int c = i >> 4, w = i & 15;
+      const u32 v = (u32)tile[4 * w][c] | ((u32)tile[4 * w + 1][c] << 8) | ((u32)tile[4 * w + 2][c] << 16) |
+                    ((u32)tile[4 * w + 3][c] << 24);
+      *reinterpret_cast<u32*>(dst + (c0 + c) * dst_ld + r0 + 4 * w) = v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      const int c = i >> 6, r = i & 63;
+      if (r0 + r < rows && c0 + c < cols) dst[(c0 + c) * dst_ld + r0 + r] = tile[r][c];
+    }
+  }
+}
 }  // namespace
 
 extern "C" {
@@ -710,6 +748,24 @@ int g9_workspace_watch(void* workspace, size_t workspace_bytes, int* host_flag, 
   void* args[] = {&w, &lo, &hi};
   return hipLaunchKernel(reinterpret_cast<const void*>(set_words2), dim3(1), dim3(64), args, 0,
                          reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? G9_OK
+             : G9_ERR_HIP;
+}
+
+int g9_transpose_u8(const void* src, int64_t rows, int64_t cols, int64_t src_ld, void* dst, int64_t dst_ld,
+                    void* stream) {
+  if (rows < 0 || cols < 0) return G9_ERR_SHAPE;
+  if (rows == 0 || cols == 0) return G9_OK;
+  if (!src || !dst || src_ld < cols || dst_ld < rows) return G9_ERR_LAYOUT;
+  if ((rows + 63) / 64 > 65535 || (cols + 63) / 64 > INT32_MAX) return G9_ERR_SHAPE;
+  const unsigned char* s = static_cast<const unsigned char*>(src);
+  unsigned char* d = static_cast<unsigned char*>(dst);
+  long long r = rows, c = cols, sl = src_ld, dl = dst_ld;
+  int words = aligned(src, 4) && aligned(dst, 4) && src_ld % 4 == 0 && dst_ld % 4 == 0;
+  void* args[] = {&s, &r, &c, &sl, &d, &dl, &words};
+  return hipLaunchKernel(reinterpret_cast<const void*>(transpose_u8), dim3((unsigned)((cols + 63) / 64),
+                                                                           (unsigned)((rows + 63) / 64)),
+                         dim3(256), args, 0, reinterpret_cast<hipStream_t>(stream)) == hipSuccess
              ? G9_OK
              : G9_ERR_HIP;
 }

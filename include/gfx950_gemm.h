@@ -250,6 +250,18 @@ int g9_workspace_watch(void* workspace, size_t workspace_bytes, int* host_flag, 
 uint32_t g9_set_streamk_spin_limit(uint32_t polls);
 
 /*
+ * Byte transpose on `stream`: dst (cols x rows, row stride dst_ld bytes) =
+ * src (rows x cols, row stride src_ld bytes) transposed.  The drop-in a4w4
+ * wrapper repacks K-major E8M0 scale views, (K/32, M) storage seen as
+ * (M, K/32), into the row-major layout the 8-wave kernels read with it
+ * (kernels/gemm/inter_wave/a4w4/bench.py:110-115 builds such views).  No
+ * counterpart in the reference.  G9_ERR_LAYOUT for null pointers or strides
+ * below the row lengths; nothing is launched when rows or cols is 0.
+ */
+int g9_transpose_u8(const void* src, int64_t rows, int64_t cols, int64_t src_ld, void* dst, int64_t dst_ld,
+                    void* stream);
+
+/*
  * Name of the kernel a call with this (dtype, out_dtype, schedule, waves)
  * launches (for G9_SCHED_SPLITK: its segment kernel, followed by
  * g9_splitk_reduce_f16 or g9_splitk_reduce_bf16 by output type),

@@ -167,3 +167,38 @@ def test_mixed_layouts_are_repacked(gpu):
     want = _run(gpu, a, b, sa.to(gpu), sb.to(gpu))
     torch.cuda.synchronize()
     assert torch.equal(c, want)
+
+
+@pytest.mark.parametrize("rows,groups,pad", [(1, 8, 0), (100, 8, 28), (4096, 256, 0), (300, 257, 212), (65, 64, 3)])
+def test_byte_transpose_matches_torch(gpu, rows, groups, pad):
+    # g9_transpose_u8 on a (groups, rows + pad) buffer seen as a (rows, groups)
+    # view: the row-major copy equals torch's, byte for byte, at ragged tile
+    # edges and with storage padding, and nothing outside the output changes.
+    _say(f"byte transpose {rows}x{groups} pad {pad}")
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(rows + groups)
+    store = torch.randint(0, 256, (groups, rows + pad), generator=gen, dtype=torch.uint8).to(gpu)
+    view = store.T[:rows]
+    out = torch.full((rows + 1, groups), 7, dtype=torch.uint8, device=gpu)
+    rc = lib.g9_transpose_u8(view.data_ptr(), groups, rows, view.stride(1), out.data_ptr(), groups,
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.G9_OK
+    torch.cuda.synchronize()
+    assert torch.equal(out[:rows], view.contiguous())
+    assert (out[rows:] == 7).all()
+
+
+def test_eight_waves_with_padded_reference_views(gpu):
+    # The reference bench's A scales: randint((K // 32, M_pad)).T[:M], M_pad a
+    # multiple of 256 (kernels/gemm/inter_wave/a4w4/bench.py:110-115).
+    M, N, K = 300, 256, 1024
+    _say(f"a4w4 8 waves, padded K-major views {M}x{N}x{K}")
+    gen = torch.Generator().manual_seed(79)
+    pa, sa = quant.quantize_mxfp4(torch.randn(M, K, generator=gen))
+    pb, sb = quant.quantize_mxfp4(torch.randn(N, K, generator=gen))
+    a, b = pa.to(gpu), pb.to(gpu)
+    # Padding rows of NaN scales (255): the repack must not read them.
+    c8 = _run(gpu, a, b, _kmajor(sa.to(gpu), pad_rows=512 - M), _kmajor(sb.to(gpu)), waves=8)
+    want = _run(gpu, a, b, sa.to(gpu), sb.to(gpu), waves=8)
+    torch.cuda.synchronize()
+    assert torch.equal(c8, want)
