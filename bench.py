@@ -19,8 +19,9 @@ read from the committed rocprof counter summary when present, the other
 dtypes, the stream-K shapes, split-K against data-parallel on grids of 16-128
 tiles, the grouped (MoE) GEMMs, the flash-attention forward (fmha_v4 and
 fmha_v3 at B=32 H=8 S=8192 D=128, bf16 and fp16, against the reference's
-published bf16 numbers), and a CPU baseline: torch.matmul in fp32 on the
-dequantized operands timed on this host on a bounded row sample.
+published bf16 numbers), the host time per launch of a one-tile GEMM (matmul
+wrapper, prepared launch, torch.matmul), and a CPU baseline: torch.matmul in
+fp32 on the dequantized operands timed on this host on a bounded row sample.
 """
 
 from __future__ import annotations
@@ -104,6 +105,8 @@ def parse_args():
                    help="energy per launch instead: ours vs hipBLASLt for fp16 and bf16, this many seconds of "
                         "back-to-back launches per side and round (two interleaved rounds), amd-smi power sampled")
     p.add_argument("--cpu-baseline", type=int, default=1)
+    p.add_argument("--launch-overhead", type=int, default=1,
+                   help="host time per launch of a one-tile GEMM: matmul wrapper, prepared launch, torch.matmul")
     p.add_argument("--rotate-mb", type=int, default=512)
     p.add_argument("--serialized", type=int, default=0,
                    help="also time serialized dispatches with HIP events (mean of the last 100 of 1000); the events "
@@ -123,6 +126,50 @@ def parse_args():
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also launch a plain device copy of this many MiB 10 times (counter calibration)")
     return p.parse_args()
+
+
+LAUNCH_SHAPE = (256, 256, 512)
+
+
+def launch_overhead(dev, calls: int = 2000) -> dict:
+    """Host time per launch (us) of a one-tile FP16 GEMM issued back to back
+    without synchronising: the a16w16 matmul wrapper, a prepared launch
+    (PreparedGemm: one g9_plan_launch call, the counterpart of the
+    reference's scripts/benchmark_prepared.py) and torch.matmul (hipBLASLt),
+    beside the GPU time per launch of the wrapper's loop.  The host side is
+    what bounds small GEMMs issued one after another."""
+    import torch
+
+    from gfx950_gluon_tutorials_amd.gemm.intra_wave.a16w16 import matmul as m16
+    from gfx950_gluon_tutorials_amd.gemm.prepared import PreparedGemm
+
+    M, N, K = LAUNCH_SHAPE
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn(M, K, generator=gen).half().to(dev)
+    bt = torch.randn(N, K, generator=gen).half().to(dev).T
+    c = torch.empty(M, N, dtype=torch.half, device=dev)
+    prep = PreparedGemm.a16w16([(a, bt, c)])
+    out = {"shape": list(LAUNCH_SHAPE), "calls": calls}
+    for name, fn in (("matmul_us", lambda: m16(a, bt, c)), ("prepared_us", prep),
+                     ("torch_matmul_us", lambda: torch.matmul(a, bt, out=c))):
+        for _ in range(100):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        host = time.perf_counter() - t0
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(host / calls * 1e6, 2)
+        if name == "matmul_us":
+            out["gpu_us_per_launch"] = round(e0.elapsed_time(e1) / calls * 1e3, 2)
+    print(f"# launch overhead, host us per call ({M}x{N}x{K} fp16, {calls} back-to-back calls): matmul "
+          f"{out['matmul_us']}, prepared {out['prepared_us']}, torch.matmul {out['torch_matmul_us']} "
+          f"(GPU {out['gpu_us_per_launch']} us per launch)", flush=True)
+    return out
 
 
 def copy_calibration(mb: int, dev) -> None:
@@ -909,6 +956,7 @@ def main():
             del launch
             torch.cuda.empty_cache()
     fmha = fmha_bench(args, dev) if args.fmha and not args.only else {}
+    overhead = launch_overhead(dev) if args.launch_overhead and not args.only else {}
     if args.copy_mb:
         copy_calibration(args.copy_mb, dev)
     head = "fp16" if "fp16" in results else next(iter(results))
@@ -937,6 +985,7 @@ def main():
         "splitk": splitk,
         "moe": moe,
         "fmha": fmha,
+        "launch_overhead": overhead,
     }
     if args.cpu_baseline and not args.only:
         line["cpu_baseline"] = cpu_baseline(M, N, K, dev, seeds)

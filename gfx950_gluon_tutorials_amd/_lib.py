@@ -27,6 +27,10 @@ G9_ERR_SCHEDULE = 4
 G9_ERR_WORKSPACE = 5
 G9_ERR_HIP = 6
 G9_ERR_SCRATCH = 7
+G9_ERR_PLAN = 8
+
+# Size of a g9_plan (G9_PLAN_BYTES in gfx950_gemm.h).
+G9_PLAN_BYTES = 512
 
 # Element types.
 G9_F16 = 0
@@ -78,6 +82,15 @@ SIGNATURES = {
     "g9_set_streamk_spin_limit": (ctypes.c_uint32, [ctypes.c_uint32]),
     "g9_transpose_u8": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "g9_noalloc_error": (_int, [_vp, ctypes.POINTER(_int)]),
+    "g9_plan_a16w16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                              _int, _int, _int, _vp, _sz]),
+    "g9_plan_a8w8": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _vp, _vp, _int, _int, _int, _vp, _sz]),
+    "g9_plan_a4w4": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz]),
+    "g9_plan_a4w4_preshuffled": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _i64, _i64, _i64, _i64, _int, _int, _int, _vp, _sz]),
+    "g9_plan_launch": (_int, [_vp, _vp]),
     "g9_kernel_name": (ctypes.c_char_p, [_int, _int, _int, _int]),
     "g9_status_string": (ctypes.c_char_p, [_int]),
     "g9_streamk_workgroups": (_int, []),
@@ -122,7 +135,7 @@ def check(code: int, what: str) -> None:
     if code == G9_OK:
         return
     msg = f"{what}: {status_text(code)} (status {code})"
-    if code in (G9_ERR_SHAPE, G9_ERR_LAYOUT, G9_ERR_DTYPE, G9_ERR_SCHEDULE):
+    if code in (G9_ERR_SHAPE, G9_ERR_LAYOUT, G9_ERR_DTYPE, G9_ERR_SCHEDULE, G9_ERR_PLAN):
         raise ValueError(msg)
     raise RuntimeError(msg)
 

@@ -3,6 +3,7 @@
 // fills a GemmParams and launches one named kernel on the caller's stream
 // (split-K: the segment kernel, then its reduction, on that stream).
 #include <atomic>
+#include <cstring>
 #include <mutex>
 
 #include "../../include/gfx950_gemm.h"
@@ -238,10 +239,27 @@ size_t splitk_bytes(long long partials) { return units_bytes(2 * partials); }
 size_t streamk_bytes(long long tiles) { return units_bytes(2 * tiles); }
 size_t streamk_half_bytes(long long tiles) { return units_bytes(tiles); }
 
+// A resolved launch: the kernel (and split-K's reduction), the grid and the
+// parameter block, i.e. everything an entry point works out before it
+// enqueues.  g9_plan_* keep it in the caller's g9_plan; run_plan only
+// enqueues it (a stream-K plan takes a new flag epoch and the current spin
+// limit at each launch).
+constexpr uint32_t kPlanMagic = 0x6c703967u;
+struct Plan {
+  uint32_t magic;
+  int device;     // the device current when the plan was made
+  int grid, block;
+  int red_grid;   // split-K reduction grid (0: no reduction)
+  int streamk;
+  const void* fn;
+  const void* red;
+  GemmParams p;
+};
+static_assert(sizeof(Plan) <= G9_PLAN_BYTES && alignof(Plan) <= alignof(g9_plan), "g9_plan cannot hold a Plan");
+
 // Shared launch path.  Sizes/strides were validated by the caller except the
 // generic checks done here.
-int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
-           void* stream) {
+int make_plan(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes, Plan& pl) {
   if (waves != 4 && waves != 8) return G9_ERR_SCHEDULE;
   if (schedule != G9_SCHED_DP && schedule != G9_SCHED_SK && schedule != G9_SCHED_SPLITK &&
       schedule != G9_SCHED_SK_HALF)
@@ -251,13 +269,14 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     return G9_ERR_SCHEDULE;
   const KernelEntry* k = find_kernel(dtype, out, schedule, waves);
   if (!k) return G9_ERR_DTYPE;
+  pl = Plan{};
+  pl.block = 64 * waves;
   const bool half = schedule == G9_SCHED_SK_HALF;
   p.tiles_m = (p.M + kTile - 1) / kTile;
   p.tiles_n = half ? (p.N + 127) / 128 : (p.N + kTile - 1) / kTile;
   p.num_xcds = kNumXcds;
   p.group_m = kGroupM;
   const long long tiles = (long long)p.tiles_m * p.tiles_n;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int grid;
   if (schedule == G9_SCHED_SPLITK) {
     const int cus = cu_count();
@@ -273,16 +292,10 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
       if (base + (size_t)(tiles * S) * kWsTileBytes > ws_bytes) return G9_ERR_WORKSPACE;
       p.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + base);
       p.split = S;
-      void* args[] = {&p};
-      if (hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3((int)(tiles * S)), dim3(64 * waves), args, 0,
-                          s) != hipSuccess)
-        return G9_ERR_HIP;
+      grid = (int)(tiles * S);
       const long long threads = (long long)p.M * p.tiles_n * (kTile / 8);
-      const KernelFn red = out == G9_BF16 ? g9_splitk_reduce_bf16 : g9_splitk_reduce_f16;
-      return hipLaunchKernel(reinterpret_cast<const void*>(red), dim3((int)((threads + 255) / 256)), dim3(256), args,
-                             0, s) == hipSuccess
-                 ? G9_OK
-                 : G9_ERR_HIP;
+      pl.red = reinterpret_cast<const void*>(out == G9_BF16 ? g9_splitk_reduce_bf16 : g9_splitk_reduce_f16);
+      pl.red_grid = (int)((threads + 255) / 256);
     }
   } else if (schedule == G9_SCHED_DP) {
     grid = (int)tiles;
@@ -299,20 +312,42 @@ int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws,
     p.err = reinterpret_cast<int*>(w);
     p.flags = reinterpret_cast<u32*>(w + kWsHeader);
     p.ws = reinterpret_cast<float*>(w + base);
-    p.epoch = (g_epoch.fetch_add(1) % 65535u) + 1u;
-    p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
     const long long units = tiles * p.ns;
     int cus = cu_count();
     if (cus <= 0) return G9_ERR_HIP;
     grid = (int)(units < cus ? units : cus);
     p.sk_ctas = grid;
+    pl.streamk = 1;
+  }
+  // Last, after every argument check, so bad arguments are reported
+  // without touching the HIP runtime.
+  if (hipGetDevice(&pl.device) != hipSuccess) return G9_ERR_HIP;
+  pl.fn = reinterpret_cast<const void*>(k->fn);
+  pl.grid = grid;
+  pl.p = p;
+  pl.magic = kPlanMagic;
+  return G9_OK;
+}
+
+int run_plan(const Plan& pl, hipStream_t s) {
+  GemmParams p = pl.p;
+  if (pl.streamk) {
+    p.epoch = (g_epoch.fetch_add(1) % 65535u) + 1u;
+    p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   }
   // hipLaunchKernel reports this launch's own status (hipGetLastError would
   // also return an earlier, unrelated error of the calling thread).
   void* args[] = {&p};
-  return hipLaunchKernel(reinterpret_cast<const void*>(k->fn), dim3(grid), dim3(64 * waves), args, 0, s) == hipSuccess
-             ? G9_OK
-             : G9_ERR_HIP;
+  if (hipLaunchKernel(pl.fn, dim3(pl.grid), dim3(pl.block), args, 0, s) != hipSuccess) return G9_ERR_HIP;
+  if (pl.red && hipLaunchKernel(pl.red, dim3(pl.red_grid), dim3(256), args, 0, s) != hipSuccess) return G9_ERR_HIP;
+  return G9_OK;
+}
+
+int launch(int dtype, int out, int schedule, int waves, GemmParams& p, void* ws, size_t ws_bytes,
+           void* stream) {
+  Plan pl;
+  const int st = make_plan(dtype, out, schedule, waves, p, ws, ws_bytes, pl);
+  return st ? st : run_plan(pl, reinterpret_cast<hipStream_t>(stream));
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int dtype, int64_t stride_cm, int64_t stride_cn,
@@ -403,24 +438,23 @@ int prep_a16w16(GemmParams& p, const void* a, const void* b, void* c, int64_t M,
 }
 }  // namespace
 
-extern "C" {
+namespace {
 
-int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
-                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
-                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
-                   void* workspace, size_t workspace_bytes, void* stream) {
+int plan_a16w16(Plan& pl, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                void* workspace, size_t workspace_bytes) {
   GemmParams p;
   const int st = prep_a16w16(p, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
                              dtype);
   if (st) return st;
-  return launch(dtype, dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+  return make_plan(dtype, dtype, schedule, waves, p, workspace, workspace_bytes, pl);
 }
 
-int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
-                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
-                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
-                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+int plan_a8w8(Plan& pl, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+              int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+              int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+              int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes) {
   if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
   int st = check_common(M, N, K, G9_BF8, stride_cm, stride_cn, c, /*allow_tail=*/true);
   if (st) return st;
@@ -441,15 +475,14 @@ int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, in
   p.ldc = stride_cm;
   p.ns = (int)((K + 127) / 128);
   p.kshift = (u32)(p.ns * 128 - K);
-  return launch(G9_BF8, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+  return make_plan(G9_BF8, out_dtype, schedule, waves, p, workspace, workspace_bytes, pl);
 }
 
-int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
-                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
-                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
-                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
-                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+int plan_a4w4(Plan& pl, const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+              int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+              int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+              int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+              int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes) {
   if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
   int st = check_common(M, N, K, G9_FP4, stride_cm, stride_cn, c);
   if (st) return st;
@@ -492,14 +525,14 @@ int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, co
   p.ldsb = (u32)stride_bsn;
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(G9_FP4));
-  return launch(dtype, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+  return make_plan(dtype, out_dtype, schedule, waves, p, workspace, workspace_bytes, pl);
 }
 
-int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
-                             int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
-                             int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
-                             int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
-                             void* workspace, size_t workspace_bytes, void* stream) {
+int plan_a4w4_preshuffled(Plan& pl, const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                          int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                          int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                          int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
+                          void* workspace, size_t workspace_bytes) {
   if (out_dtype != G9_F16 && out_dtype != G9_BF16) return G9_ERR_DTYPE;
   int st = check_common(M, N, K, G9_FP4P, stride_cm, stride_cn, c);
   if (st) return st;
@@ -533,7 +566,127 @@ int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* 
   p.ldsb = (u32)stride_bsc;
   p.ldc = stride_cm;
   p.ns = (int)(K / stage_k(G9_FP4P));
-  return launch(G9_FP4P, out_dtype, schedule, waves, p, workspace, workspace_bytes, stream);
+  return make_plan(G9_FP4P, out_dtype, schedule, waves, p, workspace, workspace_bytes, pl);
+}
+
+}  // namespace
+
+extern "C" {
+
+int g9_gemm_a16w16(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  Plan pl;
+  const int st = plan_a16w16(pl, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
+                             dtype, schedule, waves, workspace, workspace_bytes);
+  return st ? st : run_plan(pl, reinterpret_cast<hipStream_t>(stream));
+}
+
+int g9_gemm_a8w8(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  Plan pl;
+  const int st = plan_a8w8(pl, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm, stride_cn,
+                           a_scale, b_scale, out_dtype, schedule, waves, workspace, workspace_bytes);
+  return st ? st : run_plan(pl, reinterpret_cast<hipStream_t>(stream));
+}
+
+int g9_gemm_a4w4(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  Plan pl;
+  const int st = plan_a4w4(pl, a, b, c, a_scales, b_scales, M, N, K, stride_am, stride_ak, stride_bn, stride_bk,
+                           stride_cm, stride_cn, stride_asm, stride_ask, stride_bsn, stride_bsk, out_dtype, schedule,
+                           waves, workspace, workspace_bytes);
+  return st ? st : run_plan(pl, reinterpret_cast<hipStream_t>(stream));
+}
+
+int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                             int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                             int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                             int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  Plan pl;
+  const int st = plan_a4w4_preshuffled(pl, a, b, c, a_scales, b_scales, M, N, K, stride_am, stride_ak, stride_bn,
+                                       stride_bk, stride_cm, stride_cn, stride_asc, stride_bsc, out_dtype, schedule,
+                                       waves, workspace, workspace_bytes);
+  return st ? st : run_plan(pl, reinterpret_cast<hipStream_t>(stream));
+}
+
+// Prepared launches: the same validation and plan as the entry points above,
+// kept in the caller's g9_plan instead of being enqueued.
+namespace {
+int store_plan(g9_plan* out, const Plan& pl, int st) {
+  if (st) return st;
+  memcpy(out, &pl, sizeof pl);
+  return G9_OK;
+}
+}  // namespace
+
+int g9_plan_a16w16(g9_plan* plan, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes) {
+  if (!plan) return G9_ERR_PLAN;
+  Plan pl;
+  return store_plan(plan, pl,
+                    plan_a16w16(pl, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm,
+                                stride_cn, dtype, schedule, waves, workspace, workspace_bytes));
+}
+
+int g9_plan_a8w8(g9_plan* plan, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes) {
+  if (!plan) return G9_ERR_PLAN;
+  Plan pl;
+  return store_plan(plan, pl,
+                    plan_a8w8(pl, a, b, c, M, N, K, stride_am, stride_ak, stride_bk, stride_bn, stride_cm,
+                              stride_cn, a_scale, b_scale, out_dtype, schedule, waves, workspace, workspace_bytes));
+}
+
+int g9_plan_a4w4(g9_plan* plan, const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes) {
+  if (!plan) return G9_ERR_PLAN;
+  Plan pl;
+  return store_plan(plan, pl,
+                    plan_a4w4(pl, a, b, c, a_scales, b_scales, M, N, K, stride_am, stride_ak, stride_bn, stride_bk,
+                              stride_cm, stride_cn, stride_asm, stride_ask, stride_bsn, stride_bsk, out_dtype,
+                              schedule, waves, workspace, workspace_bytes));
+}
+
+int g9_plan_a4w4_preshuffled(g9_plan* plan, const void* a, const void* b, void* c, const void* a_scales,
+                             const void* b_scales, int64_t M, int64_t N, int64_t K, int64_t stride_am,
+                             int64_t stride_ak, int64_t stride_bn, int64_t stride_bk, int64_t stride_cm,
+                             int64_t stride_cn, int64_t stride_asc, int64_t stride_bsc, int out_dtype,
+                             int schedule, int waves, void* workspace, size_t workspace_bytes) {
+  if (!plan) return G9_ERR_PLAN;
+  Plan pl;
+  return store_plan(plan, pl,
+                    plan_a4w4_preshuffled(pl, a, b, c, a_scales, b_scales, M, N, K, stride_am, stride_ak, stride_bn,
+                                          stride_bk, stride_cm, stride_cn, stride_asc, stride_bsc, out_dtype,
+                                          schedule, waves, workspace, workspace_bytes));
+}
+
+int g9_plan_launch(const g9_plan* plan, void* stream) {
+  if (!plan) return G9_ERR_PLAN;
+  Plan pl;
+  memcpy(&pl, plan, sizeof pl);
+  if (pl.magic != kPlanMagic) return G9_ERR_PLAN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int dev = -1;
+  if ((s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev)) != hipSuccess) return G9_ERR_HIP;
+  if (dev != pl.device) return G9_ERR_PLAN;
+  return run_plan(pl, s);
 }
 
 int g9_moe_a16w16(const void* a, const void* b, void* c, const int32_t* expert_offsets, int64_t T,
@@ -807,6 +960,8 @@ const char* g9_status_string(int status) {
       return "HIP launch failed";
     case G9_ERR_SCRATCH:
       return "the call needs more workspace than the static scratch buffer of g9_gemm_a16w16_noalloc holds";
+    case G9_ERR_PLAN:
+      return "plan not prepared by g9_plan_*, or launched on a device other than the one it was prepared on";
   }
   return "unknown status";
 }

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import os
 import threading
+from typing import NamedTuple
 
 import torch
 
@@ -77,15 +78,17 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
-    """Returns a (K, N) view whose K stride is 1 and whose N rows start on
-    16-byte boundaries (an (N, K) row-major buffer, as the kernels' LDS-DMA
-    needs); anything else is repacked."""
+def _k_major_ok(b_kn: torch.Tensor) -> bool:
+    """A (K, N) view whose K stride is 1 and whose N rows start on 16-byte
+    boundaries (an (N, K) row-major buffer, as the kernels' LDS-DMA needs)."""
     es = b_kn.element_size()
-    if (b_kn.stride(0) == 1 and b_kn.stride(1) >= b_kn.shape[0] and b_kn.data_ptr() % 16 == 0
-            and (b_kn.stride(1) * es) % 16 == 0):
-        return b_kn
-    return b_kn.t().contiguous().t()
+    return (b_kn.stride(0) == 1 and b_kn.stride(1) >= b_kn.shape[0] and b_kn.data_ptr() % 16 == 0
+            and (b_kn.stride(1) * es) % 16 == 0)
+
+
+def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
+    """`b_kn` if _k_major_ok, else an (N, K) contiguous copy viewed as (K, N)."""
+    return b_kn if _k_major_ok(b_kn) else b_kn.t().contiguous().t()
 
 
 def _rows_ok(t: torch.Tensor) -> bool:
@@ -216,10 +219,40 @@ def _after_launch(sched: int, dev, stream: int) -> None:
         WORKSPACES.check(dev, stream)
 
 
-def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedule="dp", waves: int = 4):
-    """C = A @ B with A (M, K), B a (K, N) view, C (M, N); fp16 or bf16."""
+class _Call(NamedTuple):
+    """One resolved GEMM launch: the C entry point, its arguments up to (not
+    including) the workspace, and what the workspace size depends on."""
+    entry: str          # g9_gemm_*; the matching plan entry is g9_plan_*
+    args: tuple
+    dtype: int          # operand type code (g9_workspace_size's first argument)
+    M: int
+    N: int
+    K: int
+    schedule: int
+    waves: int
+    keep: tuple         # the tensors whose pointers are in args (repacked copies included)
+
+
+def _repack(strict: bool, what: str, make):
+    """A copy of an operand in a layout the kernels read (make()), or, for a
+    prepared launch (strict), a ValueError: a prepared launch binds the
+    caller's tensors themselves, so a hidden copy would go stale."""
+    if strict:
+        raise ValueError(f"{what} is not in a layout the kernels read in place; a prepared launch binds the "
+                         "tensors themselves, so pass it in that layout (see the matmul wrappers' docstrings)")
+    return make()
+
+
+def _run(call: _Call, dev: torch.device) -> None:
     lib = _lib.load()
-    dev = _require_device(a, b_kn, c)
+    stream = _stream(dev)
+    ws, ws_bytes = _workspace(lib, call.dtype, call.M, call.N, call.K, call.schedule, call.waves, dev, stream)
+    _lib.check(getattr(lib, call.entry)(*call.args, ws, ws_bytes, stream), call.entry)
+    _after_launch(call.schedule, dev, stream)
+
+
+def _a16w16_call(a, b_kn, c, schedule, waves, strict=False) -> _Call:
+    _require_device(a, b_kn, c)
     if a.dtype not in _DTYPE_CODE or b_kn.dtype != a.dtype or c.dtype != a.dtype:
         raise ValueError(f"a16w16 needs matching fp16/bf16 a, b, c; got {a.dtype}, {b_kn.dtype}, {c.dtype}")
     M, K = a.shape
@@ -227,17 +260,19 @@ def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedul
     if c.shape != (M, N):
         raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
     if not _rows_ok(a):
-        a = a.contiguous()
-    b_kn = _k_major(b_kn)
+        a = _repack(strict, "a", a.contiguous)
+    if not _k_major_ok(b_kn):
+        b_kn = _repack(strict, "b", lambda: _k_major(b_kn))
     dt = _DTYPE_CODE[a.dtype]
     sched = _schedule_code(schedule, M, N, dt)
-    stream = _stream(dev)
-    ws, ws_bytes = _workspace(lib, dt, M, N, K, sched, waves, dev, stream)
-    rc = lib.g9_gemm_a16w16(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
-                            a.stride(0), a.stride(1), b_kn.stride(0), b_kn.stride(1),
-                            c.stride(0), c.stride(1), dt, sched, waves, ws, ws_bytes, stream)
-    _lib.check(rc, "g9_gemm_a16w16")
-    _after_launch(sched, dev, stream)
+    args = (a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K, a.stride(0), a.stride(1), b_kn.stride(0),
+            b_kn.stride(1), c.stride(0), c.stride(1), dt, sched, waves)
+    return _Call("g9_gemm_a16w16", args, dt, M, N, K, sched, waves, (a, b_kn, c))
+
+
+def gemm_a16w16(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, schedule="dp", waves: int = 4):
+    """C = A @ B with A (M, K), B a (K, N) view, C (M, N); fp16 or bf16."""
+    _run(_a16w16_call(a, b_kn, c, schedule, waves), c.device)
     return c
 
 
@@ -251,10 +286,7 @@ def _scale_tensor(s, dev) -> torch.Tensor | None:
     return s.detach().reshape(1).to(device=dev, dtype=torch.float32)
 
 
-def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=None, b_scale=None,
-              schedule="dp", waves: int = 4):
-    """C = (A @ B) * a_scale * b_scale with BF8 (e5m2) A (M, K), B a (K, N) view."""
-    lib = _lib.load()
+def _a8w8_call(a, b_kn, c, a_scale, b_scale, schedule, waves, strict=False) -> _Call:
     dev = _require_device(a, b_kn, c)
     if a.dtype != torch.float8_e5m2 or b_kn.dtype != torch.float8_e5m2:
         raise ValueError(f"a8w8 needs float8_e5m2 operands; got {a.dtype}, {b_kn.dtype}")
@@ -265,21 +297,27 @@ def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=N
     if c.shape != (M, N):
         raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
     if not _rows_ok(a):
-        a = a.contiguous()
-    b_kn = _k_major(b_kn)
-    sa = _scale_tensor(a_scale, dev)
-    sb = _scale_tensor(b_scale, dev)
+        a = _repack(strict, "a", a.contiguous)
+    if not _k_major_ok(b_kn):
+        b_kn = _repack(strict, "b", lambda: _k_major(b_kn))
+    scales = []
+    for name, s in (("a_scale", a_scale), ("b_scale", b_scale)):
+        if strict and s is not None and not (isinstance(s, torch.Tensor) and s.dtype == torch.float32
+                                             and s.numel() == 1 and s.device == dev):
+            raise ValueError(f"a prepared a8w8 launch takes {name} as a one-element fp32 tensor on {dev} (or None)")
+        scales.append(_scale_tensor(s, dev))
+    sa, sb = scales
     sched = _schedule_code(schedule, M, N, _lib.G9_BF8)
-    stream = _stream(dev)
-    ws, ws_bytes = _workspace(lib, _lib.G9_BF8, M, N, K, sched, waves, dev, stream)
-    rc = lib.g9_gemm_a8w8(a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K,
-                          a.stride(0), a.stride(1), b_kn.stride(0), b_kn.stride(1),
-                          c.stride(0), c.stride(1),
-                          sa.data_ptr() if sa is not None else None,
-                          sb.data_ptr() if sb is not None else None,
-                          _OUT_CODE[c.dtype], sched, waves, ws, ws_bytes, stream)
-    _lib.check(rc, "g9_gemm_a8w8")
-    _after_launch(sched, dev, stream)
+    args = (a.data_ptr(), b_kn.data_ptr(), c.data_ptr(), M, N, K, a.stride(0), a.stride(1), b_kn.stride(0),
+            b_kn.stride(1), c.stride(0), c.stride(1), sa.data_ptr() if sa is not None else None,
+            sb.data_ptr() if sb is not None else None, _OUT_CODE[c.dtype], sched, waves)
+    return _Call("g9_gemm_a8w8", args, _lib.G9_BF8, M, N, K, sched, waves, (a, b_kn, c, sa, sb))
+
+
+def gemm_a8w8(a: torch.Tensor, b_kn: torch.Tensor, c: torch.Tensor, *, a_scale=None, b_scale=None,
+              schedule="dp", waves: int = 4):
+    """C = (A @ B) * a_scale * b_scale with BF8 (e5m2) A (M, K), B a (K, N) view."""
+    _run(_a8w8_call(a, b_kn, c, a_scale, b_scale, schedule, waves), c.device)
     return c
 
 
@@ -313,33 +351,25 @@ def _ps_scales_ok(s: torch.Tensor) -> bool:
     return s.stride(2) == 1 and s.stride(1) == 32 and s.stride(0) % 16 == 0 and s.data_ptr() % 16 == 0
 
 
-def _gemm_a4w4_preshuffled(lib, dev, a, b, a_scales, b_scales, c, M, N, K, schedule, waves):
+def _a4w4_preshuffled_call(a, b, a_scales, b_scales, c, M, N, K, schedule, waves, strict) -> _Call:
     chunks = -(-K // 1024)
     if a_scales.shape != (chunks, M, 32) or b_scales.shape != (chunks, N, 32):
         raise ValueError(f"preshuffled scales must be ({chunks}, {M}, 32) and ({chunks}, {N}, 32); got "
                          f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
     if not _ps_scales_ok(a_scales):
-        a_scales = a_scales.contiguous()
+        a_scales = _repack(strict, "a_scales", a_scales.contiguous)
     if not _ps_scales_ok(b_scales):
-        b_scales = b_scales.contiguous()
+        b_scales = _repack(strict, "b_scales", b_scales.contiguous)
     sched = _schedule_code(schedule, M, N, _lib.G9_FP4)
     if sched != _lib.G9_SCHED_DP or waves != 4:
         raise ValueError("preshuffled MXFP4 scales run on the 4-wave data-parallel kernel only")
-    stream = _stream(dev)
-    rc = lib.g9_gemm_a4w4_preshuffled(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(),
-                                      b_scales.data_ptr(), M, N, K, a.stride(0), a.stride(1), b.stride(0),
-                                      b.stride(1), c.stride(0), c.stride(1), a_scales.stride(0),
-                                      b_scales.stride(0), _OUT_CODE[c.dtype], sched, waves, None, 0, stream)
-    _lib.check(rc, "g9_gemm_a4w4_preshuffled")
-    return c
+    args = (a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(), M, N, K,
+            a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), a_scales.stride(0),
+            b_scales.stride(0), _OUT_CODE[c.dtype], sched, waves)
+    return _Call("g9_gemm_a4w4_preshuffled", args, _lib.G9_FP4P, M, N, K, sched, waves, (a, b, c, a_scales, b_scales))
 
 
-def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales: torch.Tensor, c: torch.Tensor,
-              *, schedule="dp", waves: int = 4):
-    """C = dequant(A) @ dequant(B)^T with packed MXFP4 A (M, K/2), B (N, K/2)
-    and E8M0 scales (M, K/32), (N, K/32), or both in the preshuffled layout
-    of quant.preshuffle_e8m0 ((ceil(K/1024), M, 32), (ceil(K/1024), N, 32);
-    4-wave data-parallel kernel)."""
+def _a4w4_call(a, b, a_scales, b_scales, c, schedule, waves, strict=False) -> _Call:
     lib = _lib.load()
     dev = _require_device(a, b, a_scales, b_scales, c)
     preshuffled = a_scales.dim() == 3
@@ -357,11 +387,11 @@ def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales
     if c.shape != (M, N):
         raise ValueError(f"c must be ({M}, {N}), got {tuple(c.shape)}")
     if not _rows_ok(a):
-        a = a.contiguous()
+        a = _repack(strict, "a", a.contiguous)
     if not _rows_ok(b):
-        b = b.contiguous()
+        b = _repack(strict, "b", b.contiguous)
     if preshuffled:
-        return _gemm_a4w4_preshuffled(lib, dev, a, b, a_scales, b_scales, c, M, N, K, schedule, waves)
+        return _a4w4_preshuffled_call(a, b, a_scales, b_scales, c, M, N, K, schedule, waves, strict)
     if a_scales.shape != (M, K // 32) or b_scales.shape != (N, K // 32):
         raise ValueError(f"scales must be ({M}, {K // 32}) and ({N}, {K // 32}); got "
                          f"{tuple(a_scales.shape)}, {tuple(b_scales.shape)}")
@@ -370,18 +400,22 @@ def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales
     kmajor = waves == 4 and _kmajor_scales_ok(a_scales) and _kmajor_scales_ok(b_scales)
     if not kmajor:
         if not _scales_ok(a_scales):
-            a_scales = _row_major_scales(lib, a_scales, dev)
+            a_scales = _repack(strict, "a_scales", lambda: _row_major_scales(lib, a_scales, dev))
         if not _scales_ok(b_scales):
-            b_scales = _row_major_scales(lib, b_scales, dev)
+            b_scales = _repack(strict, "b_scales", lambda: _row_major_scales(lib, b_scales, dev))
     dt = _lib.G9_FP4K if kmajor else _lib.G9_FP4
     sched = _schedule_code(schedule, M, N, _lib.G9_FP4)
-    stream = _stream(dev)
-    ws, ws_bytes = _workspace(lib, dt, M, N, K, sched, waves, dev, stream)
-    rc = lib.g9_gemm_a4w4(a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(),
-                          M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
-                          c.stride(0), c.stride(1), a_scales.stride(0), a_scales.stride(1),
-                          b_scales.stride(0), b_scales.stride(1), _OUT_CODE[c.dtype], sched, waves,
-                          ws, ws_bytes, stream)
-    _lib.check(rc, "g9_gemm_a4w4")
-    _after_launch(sched, dev, stream)
+    args = (a.data_ptr(), b.data_ptr(), c.data_ptr(), a_scales.data_ptr(), b_scales.data_ptr(), M, N, K,
+            a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), a_scales.stride(0),
+            a_scales.stride(1), b_scales.stride(0), b_scales.stride(1), _OUT_CODE[c.dtype], sched, waves)
+    return _Call("g9_gemm_a4w4", args, dt, M, N, K, sched, waves, (a, b, c, a_scales, b_scales))
+
+
+def gemm_a4w4(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor, b_scales: torch.Tensor, c: torch.Tensor,
+              *, schedule="dp", waves: int = 4):
+    """C = dequant(A) @ dequant(B)^T with packed MXFP4 A (M, K/2), B (N, K/2)
+    and E8M0 scales (M, K/32), (N, K/32), or both in the preshuffled layout
+    of quant.preshuffle_e8m0 ((ceil(K/1024), M, 32), (ceil(K/1024), N, 32);
+    4-wave data-parallel kernel)."""
+    _run(_a4w4_call(a, b, a_scales, b_scales, c, schedule, waves), c.device)
     return c

@@ -43,7 +43,8 @@ enum {
   G9_ERR_SCHEDULE = 4,  /* unknown schedule or wave count */
   G9_ERR_WORKSPACE = 5, /* stream-K / split-K workspace missing or too small */
   G9_ERR_HIP = 6,       /* the HIP runtime rejected the launch */
-  G9_ERR_SCRATCH = 7    /* g9_gemm_a16w16_noalloc: the call needs more than its static scratch buffer */
+  G9_ERR_SCRATCH = 7,   /* g9_gemm_a16w16_noalloc: the call needs more than its static scratch buffer */
+  G9_ERR_PLAN = 8       /* g9_plan_launch: plan not made by g9_plan_*, or made on another device */
 };
 
 /* Element / output types.  G9_FP4P is MXFP4 with preshuffled scales (the
@@ -165,6 +166,48 @@ int g9_gemm_a4w4_preshuffled(const void* a, const void* b, void* c, const void* 
                              int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
                              int64_t stride_asc, int64_t stride_bsc, int out_dtype, int schedule, int waves,
                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Prepared launches.  g9_plan_<op> takes the arguments of g9_gemm_<op>
+ * without the stream, validates them and resolves the kernel, grid and
+ * parameter block (and split-K's reduction) into *plan, returning the status
+ * g9_gemm_<op> would return, without enqueueing anything.  g9_plan_launch
+ * then only enqueues the plan on `stream`, which must belong to the device
+ * that was current when the plan was made (G9_ERR_PLAN otherwise); a
+ * stream-K plan takes a fresh flag epoch at each launch.  Each launch of a
+ * plan is the launch g9_gemm_<op> makes with the same arguments (same
+ * kernels, bit-identical results).  A plan is plain data (copyable, no
+ * destructor, nothing allocated); it holds the operand and workspace
+ * pointers, which must stay valid, and launches that share a workspace must
+ * be ordered, as for g9_gemm_<op>.
+ * Replaces the reference's prepared launches (scripts/prepared_kernel.py:53-138,
+ * used by scripts/benchmark_prepared.py:135-271), which bind each rotating
+ * argument set once so a timing loop enters the compiled launcher directly.
+ */
+#define G9_PLAN_BYTES 512
+typedef struct g9_plan {
+  uint64_t opaque[G9_PLAN_BYTES / 8];
+} g9_plan;
+
+int g9_plan_a16w16(g9_plan* plan, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                   int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                   int64_t stride_cm, int64_t stride_cn, int dtype, int schedule, int waves,
+                   void* workspace, size_t workspace_bytes);
+int g9_plan_a8w8(g9_plan* plan, const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                 int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                 int64_t stride_cm, int64_t stride_cn, const float* a_scale, const float* b_scale,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes);
+int g9_plan_a4w4(g9_plan* plan, const void* a, const void* b, void* c, const void* a_scales, const void* b_scales,
+                 int64_t M, int64_t N, int64_t K, int64_t stride_am, int64_t stride_ak,
+                 int64_t stride_bn, int64_t stride_bk, int64_t stride_cm, int64_t stride_cn,
+                 int64_t stride_asm, int64_t stride_ask, int64_t stride_bsn, int64_t stride_bsk,
+                 int out_dtype, int schedule, int waves, void* workspace, size_t workspace_bytes);
+int g9_plan_a4w4_preshuffled(g9_plan* plan, const void* a, const void* b, void* c, const void* a_scales,
+                             const void* b_scales, int64_t M, int64_t N, int64_t K, int64_t stride_am,
+                             int64_t stride_ak, int64_t stride_bn, int64_t stride_bk, int64_t stride_cm,
+                             int64_t stride_cn, int64_t stride_asc, int64_t stride_bsc, int out_dtype,
+                             int schedule, int waves, void* workspace, size_t workspace_bytes);
+int g9_plan_launch(const g9_plan* plan, void* stream);
 
 /*
  * Grouped ("MoE") GEMMs over E experts, 4-wave, data-parallel tiles.  The

@@ -52,10 +52,46 @@ def test_timing_build_exports_its_header_and_the_regular_one_does_not():
 def test_version_and_status_strings():
     lib = _lib.load()
     assert lib.g9_version() >= 100
-    for code in range(8):
+    for code in range(9):
         assert _lib.status_text(code) != "unknown status"
     assert _lib.status_text(0) == "ok"
     assert "scratch" in _lib.status_text(_lib.G9_ERR_SCRATCH)
+
+
+def test_plan_constants_match_the_header():
+    text = open(HEADER).read()
+    assert re.search(r"#define G9_PLAN_BYTES (\d+)", text).group(1) == str(_lib.G9_PLAN_BYTES)
+    assert re.search(r"G9_ERR_PLAN = (\d+)", text).group(1) == str(_lib.G9_ERR_PLAN)
+    assert "device" in _lib.status_text(_lib.G9_ERR_PLAN)
+
+
+def test_plan_launch_refuses_a_plan_no_g9_plan_call_made():
+    lib = _lib.load()
+    zero = (ctypes.c_uint64 * (_lib.G9_PLAN_BYTES // 8))()
+    assert lib.g9_plan_launch(ctypes.addressof(zero), None) == _lib.G9_ERR_PLAN
+    assert lib.g9_plan_launch(None, None) == _lib.G9_ERR_PLAN
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=0), _lib.G9_ERR_SHAPE),
+    (dict(K=100), _lib.G9_ERR_SHAPE),
+    (dict(sak=2), _lib.G9_ERR_LAYOUT),
+    (dict(dtype=_lib.G9_BF8), _lib.G9_ERR_DTYPE),
+    (dict(plan=False), _lib.G9_ERR_PLAN),
+])
+def test_plan_validates_like_the_launching_entry_point(kw, code):
+    """g9_plan_a16w16 returns g9_gemm_a16w16's status for the same bad
+    arguments, and leaves the plan unusable (nothing reaches the device)."""
+    args = dict(M=512, N=512, K=1024, sak=1, dtype=_lib.G9_F16, plan=True)
+    args.update(kw)
+    M, N, K = args["M"], args["N"], args["K"]
+    lib = _lib.load()
+    plan = (ctypes.c_uint64 * (_lib.G9_PLAN_BYTES // 8))()
+    rest = (FAKE, FAKE, FAKE, M, N, K, K, args["sak"], 1, K, N, 1, args["dtype"], _lib.G9_SCHED_DP, 4, None, 0)
+    assert lib.g9_plan_a16w16(ctypes.addressof(plan) if args["plan"] else None, *rest) == code
+    if args["plan"]:
+        assert lib.g9_gemm_a16w16(*rest, None) == code
+        assert lib.g9_plan_launch(ctypes.addressof(plan), None) == _lib.G9_ERR_PLAN
 
 
 @pytest.mark.parametrize("kw,code", [
