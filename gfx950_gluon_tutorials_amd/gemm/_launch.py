@@ -208,6 +208,8 @@ _STREAMK = (_lib.G9_SCHED_SK, _lib.G9_SCHED_SK_HALF)
 
 
 def _workspace(lib, dt: int, M: int, N: int, K: int, sched: int, waves: int, dev, stream) -> tuple[int, int]:
+    if sched == _lib.G9_SCHED_DP:
+        return 0, 0  # data-parallel launches take no workspace
     if sched in _STREAMK:
         WORKSPACES.poll(dev, stream)
     need = lib.g9_workspace_size(dt, M, N, K, sched, waves)
