@@ -105,6 +105,9 @@ def parse_args():
                    help="energy per launch instead: ours vs hipBLASLt for fp16 and bf16, this many seconds of "
                         "back-to-back launches per side and round (two interleaved rounds), amd-smi power sampled")
     p.add_argument("--cpu-baseline", type=int, default=1)
+    p.add_argument("--prepared", type=int, default=0,
+                   help="launch the per-dtype GEMM cases through PreparedGemm (arguments bound once per rotating "
+                        "set) instead of the matmul wrappers, as the reference's scripts/benchmark_prepared.py does")
     p.add_argument("--launch-overhead", type=int, default=1,
                    help="host time per launch of a one-tile GEMM: matmul wrapper, prepared launch, torch.matmul")
     p.add_argument("--rotate-mb", type=int, default=512)
@@ -186,8 +189,12 @@ def copy_calibration(mb: int, dev) -> None:
     print(f"# copy calibration: 10 x {mb} MiB device copies", flush=True)
 
 
-def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int, waves: int = 4):
-    """Returns launch(i, schedule) running the drop-in wrapper of `waves` on operand set i."""
+def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int, waves: int = 4,
+              prepared: bool = False):
+    """Returns launch(i, schedule) running the drop-in wrapper of `waves` on
+    operand set i, or with `prepared` a PreparedGemm over the sets (one per
+    schedule, bound at its first launch), as the reference's
+    scripts/benchmark_prepared.py times its kernels."""
     import torch
 
     from gfx950_gluon_tutorials_amd import quant
@@ -233,7 +240,29 @@ def make_case(dtype: str, M: int, N: int, K: int, seed: int, dev, nsets: int, wa
         else:
             m4(s[0], s[1], s[2], s[3], schedule=schedule)
 
-    return launch
+    if not prepared:
+        return launch
+    from gfx950_gluon_tutorials_amd.gemm.prepared import PreparedGemm
+
+    plans = {}
+
+    def bind(schedule):
+        if dtype in ("fp16", "bf16"):
+            return PreparedGemm.a16w16(sets, schedule=schedule, waves=waves)
+        out = [torch.empty(M, N, dtype=torch.bfloat16, device=dev) for _ in sets]
+        if dtype == "bf8":
+            return PreparedGemm.a8w8([(qa, qb, c, sa, sb) for (qa, qb, sa, sb), c in zip(sets, out)],
+                                     schedule=schedule, waves=waves)
+        return PreparedGemm.a4w4([(pa, pb, sa, sb, c) for (pa, pb, sa, sb), c in zip(sets, out)],
+                                 schedule=schedule, waves=waves)
+
+    def launch_prepared(i, schedule="dp"):
+        p = plans.get(schedule)
+        if p is None:
+            p = plans[schedule] = bind(schedule)
+        p(i)
+
+    return launch_prepared
 
 
 def set_bytes(dtype, M, N, K):
@@ -832,12 +861,13 @@ def main():
                           if not (dt in FOUR_WAVE_ONLY and w == 8)]
     for dt, kk, w, ref, rotate_mb in cases:
         nsets = max(2, -(-rotate_mb * 2**20 // set_bytes(dt, M, N, kk)))
-        launch = make_case(dt, M, N, kk, seeds[dt], dev, nsets, w)
+        launch = make_case(dt, M, N, kk, seeds[dt], dev, nsets, w, prepared=bool(args.prepared))
         ms = time_case(launch, args.steps, args.warmup, settle_s=args.settle_ms / 1e3)
         tf = 2.0 * M * N * kk / (ms * 1e-3) / 1e12
         key = dt + ("" if kk == K else f"_k{kk}") + ("" if w == 4 else "_8w")
         results[key] = {"tflops": round(tf, 2), "ms": round(ms, 5), "frac_of_peak": round(tf / PEAK[dt], 4),
-                        "reference_tflops": ref, "K": kk, "rotating_sets": nsets, "waves": w}
+                        "reference_tflops": ref, "K": kk, "rotating_sets": nsets, "waves": w,
+                        "launch": "prepared" if args.prepared else "matmul"}
         if dt in SCALE_LAYOUTS:
             results[key]["scales"] = SCALE_LAYOUTS[dt]
         msg = f"# {key}: {ms * 1e3:.1f} us  {tf:.1f} TFLOPS  {100 * tf / PEAK[dt]:.1f}% of peak"
