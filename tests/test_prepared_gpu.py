@@ -175,3 +175,31 @@ def test_c_abi_plan_is_plain_data(gpu):
     assert lib.g9_plan_launch(ctypes.addressof(zero), stream) == _lib.G9_ERR_PLAN
     torch.cuda.synchronize()
     np.testing.assert_array_equal(_bits(c), _bits(c_ref))
+
+
+@pytest.mark.parametrize("schedule,M,N,K", [("dp", 1000, 700, 2048), ("splitk", 512, 1024, 4096)])
+def test_prepared_launches_replay_in_a_graph(gpu, schedule, M, N, K):
+    """Two slots' launches captured in one HIP graph (a plan launch is a bare
+    hipLaunchKernel, split-K's two kernels included) and replayed three
+    times with eager work and synchronisations in between: every replay
+    matches the wrappers' eager output bit for bit."""
+    _say(f"prepared {schedule} {M}x{N}x{K} captured in a graph")
+    sets = _f16_sets(gpu, M, N, K, torch.float16, 2, 99)
+    want = [_launch.gemm_a16w16(a, b, torch.empty_like(c), schedule=schedule) for a, b, c in sets]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=gpu)
+    with torch.cuda.stream(side):
+        prep = PreparedGemm.a16w16(sets, schedule=schedule)  # bound to `side`
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        prep(0)
+        prep(1)
+    for r in range(3):
+        for _, _, c in sets:
+            c.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for (_, _, c), w in zip(sets, want):
+            assert torch.equal(c, w), r
