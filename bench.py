@@ -986,7 +986,13 @@ def main():
             del launch
             torch.cuda.empty_cache()
     fmha = fmha_bench(args, dev) if args.fmha and not args.only else {}
-    overhead = launch_overhead(dev) if args.launch_overhead and not args.only else {}
+    overhead = {}
+    if args.launch_overhead and not args.only:
+        try:  # an auxiliary figure: a failure here must not cost the headline line
+            overhead = launch_overhead(dev)
+        except Exception as e:  # noqa: BLE001 (reported in the JSON line instead)
+            overhead = {"error": f"{type(e).__name__}: {e}"}
+            print(f"# launch overhead not measured: {overhead['error']}", flush=True)
     if args.copy_mb:
         copy_calibration(args.copy_mb, dev)
     head = "fp16" if "fp16" in results else next(iter(results))
