@@ -394,6 +394,29 @@ def operand_study(kinds, M: int = 4096, N: int = 4096, K: int = 8192, waves: int
     return out
 
 
+KERNEL_BASE = {"fp16": "g9_a16w16_f16", "bf16": "g9_a16w16_bf16", "bf8": "g9_a8w8_bf16out",
+               "mxfp4": "g9_a4w4_bf16out", "mxfp4km": "g9_a4w4km_bf16out", "mxfp4ps": "g9_a4w4ps_bf16out"}
+
+
+def perf_table(results: list[dict], resources_path: str) -> str:
+    """The reference's perf table (scripts/run_perf_table.py:265-391, printed
+    as in scripts/README.md: TFLOPS | VGPRs | Spills | MFMA Eff.), one row per
+    measured data-parallel kernel, registers and spills from the regular
+    build's code-object table (``<lib>.resources.json``, which the timing
+    build's kernels match: the stamps add no registers to the loop)."""
+    with open(resources_path) as f:
+        res = {r["kernel"]: r for r in json.load(f)}
+    lines = ["| Kernel | M x N x K | TFLOPS | VGPRs | Spills | MFMA Eff. |",
+             "|---|---|---|---|---|---|"]
+    for r in results:
+        name = f"{KERNEL_BASE[r['dtype']]}_dp_{r['waves']}w"
+        k = res.get(name, {})
+        spills = k.get("vgpr_spill", 0) + k.get("sgpr_spill", 0) if k else "?"
+        lines.append(f"| {name} | {r['M']}x{r['N']}x{r['K']} | {r['tflops']:.0f} | {k.get('vgpr_total', '?')} | "
+                     f"{spills} | {100 * r['mfma_efficiency']:.2f}% |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--dtypes", default="fp16,bf8,mxfp4")
@@ -402,6 +425,8 @@ def main(argv=None) -> int:
     ap.add_argument("--K", default="8192", help="comma-separated list")
     ap.add_argument("--waves", default="4")
     ap.add_argument("--json", help="also write the results to this file")
+    ap.add_argument("--table", action="store_true",
+                    help="also print the reference's perf table (TFLOPS, VGPRs, spills, MFMA efficiency) in markdown")
     ap.add_argument("--streamk", action="store_true",
                     help="stream-K fixup cost instead (give --M/--N/--K; e.g. 8192 1280 8192)")
     ap.add_argument("--fmha", help="flash-attention forward instead: B,H,S[,D] (e.g. 32,8,8192; D 128 or 64); "
@@ -468,6 +493,10 @@ def main(argv=None) -> int:
                       f"{min(r['xcd_clock_ghz']):.3f}-{max(r['xcd_clock_ghz']):.3f} GHz, median end "
                       f"{min(r['xcd_end_us']):.1f}-{max(r['xcd_end_us']):.1f} us",
                       flush=True)
+    if args.table:
+        from . import build as _b
+
+        print(perf_table(results, _b.LIB_PATH + ".resources.json"), flush=True)
     if args.json:
         with open(args.json, "w") as f:
             json.dump(results, f, indent=1)

@@ -88,3 +88,18 @@ def test_operand_study_kinds():
     assert torch.all(a == a[:, :1]) and torch.all(b == b[:, :1])
     with pytest.raises(ValueError):
         profiling._study_operands("uniform", 8, 8, 32, g)
+
+
+def test_perf_table_rows_take_registers_from_the_build(tmp_path):
+    """The reference's table columns, one row per measured kernel, registers
+    and spills looked up by kernel name in the build's resource table."""
+    res = tmp_path / "lib.so.resources.json"
+    res.write_text('[{"kernel": "g9_a16w16_f16_dp_4w", "agpr": 256, "vgpr_total": 512, "sgpr": 80, '
+                   '"vgpr_spill": 0, "sgpr_spill": 0, "scratch_bytes": 0, "lds_bytes": 135168}]')
+    rows = [{"dtype": "fp16", "waves": 4, "M": 4096, "N": 4096, "K": 8192, "tflops": 1481.2, "mfma_efficiency": 0.9421},
+            {"dtype": "mxfp4km", "waves": 4, "M": 4096, "N": 4096, "K": 8192, "tflops": 4772.0,
+             "mfma_efficiency": 0.884}]
+    table = profiling.perf_table(rows, str(res)).splitlines()
+    assert table[0] == "| Kernel | M x N x K | TFLOPS | VGPRs | Spills | MFMA Eff. |"
+    assert table[2] == "| g9_a16w16_f16_dp_4w | 4096x4096x8192 | 1481 | 512 | 0 | 94.21% |"
+    assert table[3] == "| g9_a4w4km_bf16out_dp_4w | 4096x4096x8192 | 4772 | ? | ? | 88.40% |"
