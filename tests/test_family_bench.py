@@ -31,3 +31,16 @@ def test_every_family_module_has_a_bench_entry():
         for fam in ("a16w16", "a8w8", "a4w4"):
             m = importlib.import_module(f"gfx950_gluon_tutorials_amd.gemm.{route}.{fam}.bench")
             assert m.NUM_WARPS == (4 if route == "intra_wave" else 8)
+
+
+def test_attention_bench_options():
+    from gfx950_gluon_tutorials_amd.attention import bench as ab
+
+    a = ab.parse_args([])
+    assert (a.dtype, a.layout, a.batch, a.hq, a.hk, a.d, a.seqlen, a.n_iters) == ("bf16", "bhsd", 1, 64, 64, 128,
+                                                                                   8192, 1000)
+    assert ab.SEQLENS == [1024, 2048, 4096, 8192, 16384]  # kernels/attention/bench.py:99
+    # One set of B=1, HQ=HK=64, S=1024, D=128 bf16 holds 64 MiB: 8 sets span 512 MiB; S=16384 needs one.
+    assert ab.rotating_set_count(ab.parse_args(["--seqlen", "1024"]), 1024) == 8
+    assert ab.rotating_set_count(ab.parse_args([]), 16384) == 1
+    assert ab.rotating_set_count(ab.parse_args(["--rotating-sets", "3"]), 1024) == 3

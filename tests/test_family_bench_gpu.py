@@ -26,3 +26,17 @@ def test_family_bench_checks_and_times(gpu, capsys, route, fam):
     assert fb.main(fam, m.matmul, m.NUM_WARPS, ["--K", str(SMALL_K[fam]), "--rocprof", "--iters", "5",
                                                  "--rotating-buffer-size", "64"]) == 0
     assert "5 iterations done" in capsys.readouterr().out
+
+
+@pytest.mark.parametrize("extra", [["--layout", "bshd", "--hq", "8", "--hk", "2", "--d", "64", "--dtype", "fp16"],
+                                   ["--hq", "4", "--hk", "4", "--variant", "3"]])
+def test_attention_bench_checks_times_and_rocprof(gpu, capsys, extra):
+    from gfx950_gluon_tutorials_amd.attention import bench as ab
+
+    print(f"\n[case] attention bench {extra}", flush=True)
+    assert ab.main(["--seqlen", "1024", *extra]) == 0
+    out = capsys.readouterr().out
+    assert ": match" in out and "MISMATCH" not in out
+    assert any(ln.startswith("1024 ") and float(ln.split()[1]) > 0 for ln in out.splitlines())
+    assert ab.main(["--seqlen", "1024", "--rocprof", "--n-iters", "4", "--rotating-sets", "2", *extra]) == 0
+    assert "4 iterations done (2 rotating set(s))" in capsys.readouterr().out
