@@ -477,7 +477,12 @@ def summarize_rocpd(path: str) -> None:
 
     dbs = sorted(glob.glob(os.path.join(path, "**", "*.db"), recursive=True))
     if not dbs:
-        print(f"no rocprofv3 databases under {path}")
+        csvs = sorted(glob.glob(os.path.join(path, "**", "*_kernel_trace.csv"), recursive=True)
+                      + glob.glob(os.path.join(path, "**", "*_counter_collection.csv"), recursive=True))
+        if not csvs:
+            print(f"no rocprofv3 databases or CSV files under {path}")
+        for f in csvs:
+            summarize_csv(f, path)
         return
     for db in dbs:
         con = sqlite3.connect(db)
@@ -527,6 +532,64 @@ def summarize_rocpd(path: str) -> None:
                 n = len(g["dur"]) // max(1, len(g) - 1)
                 vals = "  ".join(f"{cn}={st.median(v):.6g}" for cn, v in sorted(g.items()) if cn != "dur")
                 print(f"{name[:48]:48s} grid={grid} dispatches={n} median_us={st.median(g['dur']):.2f}  {vals}")
+
+
+def _runs(rows):
+    """Groups (name, grid, payload) rows in dispatch order by kernel and grid,
+    one group per consecutive run of a GEMM kernel (the same kernel at two
+    shapes gives two groups, the later one suffixed #2; the split-K
+    reduction, launched after every split-K launch, does not end a run)."""
+    groups, runs, last = {}, {}, None
+    for name, grid, payload in rows:
+        key = (name, grid)
+        if name.startswith("g9_") and "splitk_reduce" not in name and key != last:
+            runs[key] = runs.get(key, 0) + 1
+            last = key
+        n = runs.get(key, 1)
+        groups.setdefault((name if n == 1 else f"{name}#{n}", grid), []).append(payload)
+    return groups
+
+
+def summarize_csv(f: str, root: str) -> None:
+    """The same summary from rocprofv3's CSV output (``--output-format csv``
+    / ``-f csv``, as the reference's protocol runs it): a kernel trace
+    (``*_kernel_trace.csv``: durations) or a counter collection
+    (``*_counter_collection.csv``: per-dispatch counter medians)."""
+    import csv
+    import statistics as st
+
+    with open(f, newline="") as fh:
+        rows = list(csv.DictReader(fh))
+    print(f"== {os.path.relpath(f, root)}")
+    if not rows:
+        return
+
+    def grid(r):
+        return int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0) * int(r.get("Grid_Size_Y") or 1) * \
+            int(r.get("Grid_Size_Z") or 1)
+
+    def order(r):
+        return int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0), int(r.get("Start_Timestamp") or 0)
+
+    rows.sort(key=order)
+    if "Counter_Name" not in rows[0]:
+        groups = _runs((r["Kernel_Name"], grid(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                       for r in rows)
+        print(f"{'kernel':48s} {'grid':>8s} {'calls':>6s} {'mean_us':>9s} {'median_us':>9s} "
+              f"{'min_us':>8s} {'max_us':>8s} {'last100_mean_us':>15s}")
+        for (name, g), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            print(f"{name[:48]:48s} {g:8d} {len(d):6d} {st.mean(d):9.2f} {st.median(d):9.2f} "
+                  f"{min(d):8.2f} {max(d):8.2f} {st.mean(d[-100:]):15.2f}")
+        return
+    groups = _runs((r["Kernel_Name"], grid(r), r) for r in rows)
+    for (name, g), rs in sorted(groups.items(), key=lambda kv: -len(kv[1])):
+        by_counter, durs = {}, {}
+        for r in rs:
+            by_counter.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            durs[r.get("Dispatch_Id") or r["Start_Timestamp"]] = (int(r["End_Timestamp"]) -
+                                                                 int(r["Start_Timestamp"])) / 1e3
+        vals = "  ".join(f"{cn}={st.median(v):.6g}" for cn, v in sorted(by_counter.items()))
+        print(f"{name[:48]:48s} grid={g} dispatches={len(durs)} median_us={st.median(durs.values()):.2f}  {vals}")
 
 
 def streamk_fixups(tiles: int, stages: int, ctas: int) -> int:

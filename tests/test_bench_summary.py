@@ -44,3 +44,39 @@ def test_summary_groups(tmp_path, capsys):
     assert out["g9_a16w16_f16_splitk_4w#2@65536"][2] == "2"
     assert out["g9_splitk_reduce_f16@131072"][2] == "4"
     assert out["g9_splitk_reduce_f16@262144"][2] == "2"
+
+
+def test_csv_kernel_trace_and_counters(tmp_path, capsys):
+    """The same grouping from rocprofv3's CSV output (the reference's protocol
+    writes CSV): a kernel trace gives durations, a counter collection the
+    per-dispatch medians of every counter."""
+    import csv
+
+    trace = tmp_path / "kt_kernel_trace.csv"
+    rows = [("g9_a16w16_f16_dp_4w", 65536, 180)] * 3 + [("g9_a16w16_f16_dp_4w", 4096, 120)] * 2 \
+        + [("g9_a16w16_f16_dp_4w", 65536, 200)] * 2
+    with open(trace, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kind", "Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp",
+                    "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"])
+        t = 0
+        for i, (n, g, us) in enumerate(rows):
+            w.writerow(["KERNEL_DISPATCH", i + 1, n, t, t + us * 1000, g, 1, 1])
+            t += us * 1000 + 5000
+    pmc = tmp_path / "p_counter_collection.csv"
+    with open(pmc, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value",
+                    "Start_Timestamp", "End_Timestamp"])
+        for d in range(4):
+            for cn, v in (("FETCH_SIZE", 100 + d), ("WRITE_SIZE", 50)):
+                w.writerow([d + 1, 65536, "g9_a4w4_bf16out_dp_4w", cn, v, d * 100000, d * 100000 + 60000])
+    bench.summarize_rocpd(str(tmp_path))
+    out = capsys.readouterr().out
+    lines = {l.split()[0] + "@" + l.split()[1]: l.split() for l in out.splitlines() if l.startswith("g9_a16w16")}
+    assert lines["g9_a16w16_f16_dp_4w@65536"][2:4] == ["3", "180.00"]
+    assert lines["g9_a16w16_f16_dp_4w#2@65536"][2:4] == ["2", "200.00"]
+    assert lines["g9_a16w16_f16_dp_4w@4096"][2] == "2"
+    pm = [l for l in out.splitlines() if l.startswith("g9_a4w4")]
+    assert pm == ["g9_a4w4_bf16out_dp_4w                            grid=65536 dispatches=4 median_us=60.00  "
+                  "FETCH_SIZE=101.5  WRITE_SIZE=50"]
