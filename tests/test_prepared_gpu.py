@@ -177,12 +177,15 @@ def test_c_abi_plan_is_plain_data(gpu):
     np.testing.assert_array_equal(_bits(c), _bits(c_ref))
 
 
-@pytest.mark.parametrize("schedule,M,N,K", [("dp", 1000, 700, 2048), ("splitk", 512, 1024, 4096)])
+@pytest.mark.parametrize("schedule,M,N,K", [("dp", 1000, 700, 2048), ("splitk", 512, 1024, 4096),
+                                            ("streamk", 1300, 1100, 2048), ("streamk_half", 600, 900, 1536)])
 def test_prepared_launches_replay_in_a_graph(gpu, schedule, M, N, K):
     """Two slots' launches captured in one HIP graph (a plan launch is a bare
     hipLaunchKernel, split-K's two kernels included) and replayed three
     times with eager work and synchronisations in between: every replay
-    matches the wrappers' eager output bit for bit."""
+    matches the wrappers' eager output bit for bit.  A captured stream-K
+    launch keeps the flag epoch it was captured with; every tile's last
+    owner clears its flag, so each replay starts from clear flags."""
     _say(f"prepared {schedule} {M}x{N}x{K} captured in a graph")
     sets = _f16_sets(gpu, M, N, K, torch.float16, 2, 99)
     want = [_launch.gemm_a16w16(a, b, torch.empty_like(c), schedule=schedule) for a, b, c in sets]
@@ -203,3 +206,4 @@ def test_prepared_launches_replay_in_a_graph(gpu, schedule, M, N, K):
         torch.cuda.synchronize()
         for (_, _, c), w in zip(sets, want):
             assert torch.equal(c, w), r
+    assert prep.error() == 0
