@@ -300,3 +300,29 @@ def test_auto_schedule_rule():
     assert _launch.auto_schedule(4352, 4096, cus=256, dtype=_lib.G9_BF16) == sk
     for dt in (_lib.G9_BF8, _lib.G9_FP4):  # fewer K stages per tile: stream-K measured slower
         assert _launch.auto_schedule(4352, 4096, cus=256, dtype=dt) == dp
+
+
+def test_headers_compile_as_c_and_cpp(tmp_path):
+    """The headers are plain C (C99 and C++17), and a C caller can size a
+    g9_plan on its stack and pass it to the plan entry points."""
+    import shutil
+    import subprocess
+
+    src = tmp_path / "use.c"
+    src.write_text(
+        '#include "gfx950_gemm.h"\n#include "gfx950_fmha.h"\n'
+        "int use(const void* a, const void* b, void* c, void* stream) {\n"
+        "  g9_plan plan;\n"
+        "  int rc = g9_plan_a16w16(&plan, a, b, c, 256, 256, 512, 512, 1, 1, 512, 256, 1, G9_F16, G9_SCHED_DP, 4,\n"
+        "                          0, 0);\n"
+        "  return rc ? rc : g9_plan_launch(&plan, stream);\n"
+        "}\n"
+        "typedef char plan_size_ok[sizeof(g9_plan) == G9_PLAN_BYTES ? 1 : -1];\n")
+    inc = os.path.dirname(HEADER)
+    for compiler, std in (("gcc", "-std=c99"), ("g++", "-std=c++17")):
+        if not shutil.which(compiler):
+            pytest.skip(f"{compiler} not found")
+        lang = ["-x", "c++"] if compiler == "g++" else []
+        r = subprocess.run([compiler, std, "-Wall", "-Werror", "-fsyntax-only", "-I", inc, *lang, str(src)],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
